@@ -1,0 +1,312 @@
+#!/usr/bin/env python
+"""Benchmark of the MXFP4 hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+
+Prints ONE JSON line.  The headline (``value``) is BASELINE config 2's
+prefill point: the dense W4A16 linear at qkv_proj shape M=4096, K=2048,
+N=5120 (bf16 activations ~N(0,1), E2M1 codes uniform 0..15, E8M0 scales
+uniform 120..128, seeded), in TFLOP/s.  A step is one
+``linear_mxfp4_soft`` call on HBM-resident inputs; K steps are timed with a
+device synchronisation on both sides.  ``roofline`` is for that step's only
+kernel (w4a16_tiled), its average duration taken from HIP events on the
+stream it is launched on.  ``sweep`` carries the other BASELINE points:
+decode W4A16 GEMV (HBM GB/s, weights rotated over >= 512 MB so the 256 MB
+MALL cannot serve them, launches replayed from a HIP graph), the routed MoE
+layer (us), W4A4 on the block-scaled FP4 MFMA, and the standalone dequant.
+``cpu_baseline`` times the reference safe path (explicit dequant +
+torch.matmul bf16, restated in oracle/) on this host's cores on a bounded
+row sample of the headline workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "mxfp4-gfx936_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP4_PEAK_TFLOPS = 10100.0
+METRIC = ("W4A16 GEMM TFLOP/s (prefill) & HBM GB/s (decode), % roofline; MoE layer µs")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def rand_weights(rng, rows, k, copies=1):
+    import numpy as np
+    import torch
+    out = []
+    for _ in range(copies):
+        p = torch.from_numpy(rng.integers(0, 256, size=(*rows, k // 2), dtype=np.uint8)).cuda()
+        s = torch.from_numpy(rng.integers(120, 129, size=(*rows, k // 32), dtype=np.uint8)).cuda()
+        out.append((p, s))
+    return out
+
+
+def randn_bf16(seed, shape):
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(torch.bfloat16).cuda()
+
+
+def time_eager(fn, steps, warmup):
+    """(wall ms per step, HIP-event ms per step) over `steps` calls."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, start.elapsed_time(end) / steps
+
+
+def time_graph(fns, replays=20):
+    """Capture one call of each fn (rotating inputs) in a HIP graph; return
+    the device time per call (ms), from events around graph replays."""
+    import torch
+    for f in fns:  # warm up outside capture (allocator, library load)
+        f()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for f in fns:
+                f()
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * len(fns))
+
+
+def linear_bytes(m, n, k):
+    return n * k // 2 + n * k // 32 + 2 * m * k + 2 * m * n
+
+
+def sweep(mx, torch, np):
+    res = {}
+    # --- decode / mid W4A16
+    for name, k, n in (("qkv", 2048, 5120), ("o_proj", 4096, 2048)):
+        for m in (1, 8, 370) + ((4096,) if name == "o_proj" else ()):
+            rng = np.random.default_rng(20260811 + m + k)
+            wbytes = n * k // 2 + n * k // 32
+            copies = max(1, min(128, (600 << 20) // wbytes)) if m <= 370 else 1
+            ws = rand_weights(rng, (n,), k, copies)
+            x = randn_bf16(20260811 + m, (m, k))
+            fns = [lambda p=p, s=s: mx.linear_mxfp4_soft(x, p, s) for p, s in ws]
+            if m <= 370:
+                t = time_graph(fns, replays=10)
+            else:
+                t = time_eager(fns[0], 20, 5)[1]
+            b = linear_bytes(m, n, k)
+            fl = 2.0 * m * n * k
+            res[f"w4a16_{name}_m{m}"] = {
+                "us": round(t * 1e3, 3), "GB/s": round(b / t / 1e6, 1),
+                "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4),
+                "TFLOP/s": round(fl / t / 1e9, 2),
+                "mfma_frac": round(fl / t / 1e9 / BF16_PEAK_TFLOPS, 4),
+                "weight_copies": copies}
+            log(f"{name} m={m}: {res[f'w4a16_{name}_m{m}']}")
+            del ws
+    torch.cuda.empty_cache()
+    # --- routed MoE layer (BASELINE configs 3 and 5)
+    e, hidden, inter, top_k = 128, 2048, 768, 8
+    rng = np.random.default_rng(20260815)
+    layer_copies = []
+    for _ in range(3):
+        (w13, s13), = rand_weights(rng, (e, 2 * inter), hidden)
+        (w2, s2), = rand_weights(rng, (e, hidden), inter)
+        layer_copies.append((w13, s13, w2, s2))
+    per_expert = 2 * inter * hidden // 2 + 2 * inter * hidden // 32 + hidden * inter // 2 + \
+        hidden * inter // 32
+    for m in (1, 8, 32, 512, 4096):
+        g = torch.Generator().manual_seed(20260817 + m)
+        logits = torch.randn((m, e), generator=g)
+        w, ids = torch.topk(torch.softmax(logits, -1), top_k, dim=-1)
+        w = (w / w.sum(-1, keepdim=True)).cuda()
+        ids = ids.cuda()
+        x = randn_bf16(20260816 + m, (m, hidden))
+        e_active = int(torch.unique(ids).numel())
+        fns = [lambda c=c: mx.moe_layer(x, *c, w, ids) for c in layer_copies]
+        if m <= 512:
+            t = time_graph(fns, replays=10)
+        else:
+            t = time_eager(fns[0], 10, 3)[1]
+        b = e_active * per_expert + 4 * m * hidden + 8 * m * top_k
+        fl = 2.0 * m * top_k * (hidden * 2 * inter + inter * hidden)
+        res[f"moe_layer_m{m}"] = {
+            "us": round(t * 1e3, 2), "e_active": e_active, "GB/s": round(b / t / 1e6, 1),
+            "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4), "TFLOP/s": round(fl / t / 1e9, 2),
+            "mfma_frac": round(fl / t / 1e9 / BF16_PEAK_TFLOPS, 4)}
+        log(f"moe m={m}: {res[f'moe_layer_m{m}']}")
+    del layer_copies
+    torch.cuda.empty_cache()
+    # --- W4A4, activations/weights quantized with the RNE rule
+    m, k, n = 8192, 4096, 4096
+    a = randn_bf16(4, (m, k))
+    wt = (randn_bf16(5, (n, k)).float() * 0.02)
+    ap, asc = mx.dynamic_mxfp4_quant(a, "rne")
+    wp, wsc = mx.dynamic_mxfp4_quant(wt, "rne")
+    t = time_eager(lambda: mx.linear_mxfp4_w4a4(ap, asc, wp, wsc), 20, 5)[1]
+    fl = 2.0 * m * n * k
+    res["w4a4_8192x4096x4096"] = {"us": round(t * 1e3, 2), "TFLOP/s": round(fl / t / 1e9, 1),
+                                  "fp4_frac": round(fl / t / 1e9 / FP4_PEAK_TFLOPS, 4)}
+    log(f"w4a4: {res['w4a4_8192x4096x4096']}")
+    tq = time_eager(lambda: mx.dynamic_mxfp4_quant(a, "rne"), 20, 5)[1]
+    qb = m * k * 2 + m * k // 2 + m * k // 32
+    res["quant_rne_8192x4096"] = {"us": round(tq * 1e3, 2), "GB/s": round(qb / tq / 1e6, 1)}
+    # --- standalone dequant: all 128 experts' w13 -> bf16
+    (p, s), = rand_weights(np.random.default_rng(9), (128 * 1536,), 2048)
+    t = time_eager(lambda: mx.dequant_mxfp4(p, s, torch.bfloat16), 10, 3)[1]
+    db = p.numel() + s.numel() + p.numel() * 4
+    res["dequant_bf16_128x1536x2048"] = {"us": round(t * 1e3, 1), "GB/s": round(db / t / 1e6, 1),
+                                         "hbm_frac": round(db / t / 1e6 / HBM_PEAK_GBS, 4)}
+    log(f"dequant: {res['dequant_bf16_128x1536x2048']}")
+    return res
+
+
+def cpu_baseline(np, m, k, n, budget_s=20.0):
+    """The reference safe path restated (oracle/mxfp4_oracle.py: explicit
+    dequant -> torch.matmul bf16), timed on this host on a row sample."""
+    import torch
+    from oracle import mxfp4_oracle as O
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():  # the host share given to this job
+        threads = max(1, min(threads, int(os.environ["OMP_NUM_THREADS"])))
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(20260812)
+    w = torch.from_numpy(rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8))
+    s = torch.from_numpy(rng.integers(120, 129, size=(n, k // 32), dtype=np.uint8))
+    probe_m = 64
+    x = torch.randn((probe_m, k), generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    O.linear_safe(x, w, s)  # warm-up
+    t0 = time.perf_counter()
+    O.linear_safe(x, w, s)
+    t_probe = time.perf_counter() - t0
+    # rows so that one call takes about budget/6, capped at the workload's M
+    rows = int(min(m, max(probe_m, probe_m * (budget_s / 6) / max(t_probe, 1e-3))))
+    x = torch.randn((rows, k), generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    O.linear_safe(x, w, s)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        O.linear_safe(x, w, s)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    flops = 2.0 * rows * n * k
+    isa = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = next((ln for ln in f if ln.startswith("flags")), "")
+        isa = ",".join(x for x in ("avx512_bf16", "amx_bf16", "avx512f", "avx2") if x in flags.split())
+    except OSError:
+        pass
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"safe path (dequant + torch.matmul bf16) on x[{rows},{k}] x W[{n},{k}], "
+                      f"median of {len(times)} calls ({t * 1e3:.1f} ms each), torch "
+                      f"{torch.__version__}, isa {isa}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import mxfp4_amd as mx
+    mx._lib.load()
+    torch.cuda.set_device(0)
+
+    m, k, n = 4096, 2048, 5120
+    rng = np.random.default_rng(20260810 + 1)
+    (w, s), = rand_weights(rng, (n,), k)
+    x = randn_bf16(20260810, (m, k))
+    log(f"headline: w4a16 linear m={m} k={k} n={n}, warmup {args.warmup}, steps {args.steps}")
+    for _ in range(args.warmup):
+        mx.linear_mxfp4_soft(x, w, s)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        mx.linear_mxfp4_soft(x, w, s)
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    kernel_ms = start.elapsed_time(end) / args.steps
+    flops = 2.0 * m * n * k
+    value = flops / (wall_ms * 1e-3) / 1e12
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    log(f"headline: {wall_ms:.4f} ms/step wall, {kernel_ms:.4f} ms/kernel, {value:.1f} TFLOP/s")
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded: E2M1 codes uniform 0..15, E8M0 120..128, x ~ N(0,1) bf16)",
+        "config": {"workload": "w4a16_linear_qkv_prefill", "m": m, "k": k, "n": n,
+                   "op": "linear_mxfp4_soft", "weights": "MXFP4 E2M1 + E8M0/32",
+                   "activations": "bf16"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel": "w4a16_tiled<bf16,4,4,STORE>",
+                     "kernel_us": round(kernel_ms * 1e3, 3),
+                     "algorithmic_bytes": linear_bytes(m, n, k)},
+    }
+    if not args.no_sweep:
+        out["sweep"] = sweep(mx, torch, np)
+    if not args.no_cpu:
+        log("cpu baseline (bounded sample)")
+        out["cpu_baseline"] = cpu_baseline(np, m, k, n)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,179 @@
+/*
+ * libmxfp4_gfx950 -- C ABI of the MI355X (gfx950) MXFP4 backend.
+ *
+ * Drop-in replacement for the `moe_op_mxfp4_soft` operator surface of
+ * lutianshu824/mxfp4-gfx936.  Reference paths below are relative to that
+ * repository:
+ *   soft  = src/aiter/ops/triton/moe_op_mxfp4_soft.py
+ *   aiter = integration/aiter/moe_op_mxfp4.py
+ *   vllm  = integration/vllm/vllm_mxfp4_gfx936.py
+ *   test  = tests/test_moe_mxfp4_soft.py
+ *
+ * Conventions
+ *   - Every pointer argument is device memory on the current HIP device,
+ *     except where a comment says otherwise.  The caller owns all memory; the
+ *     library allocates nothing on the device and never synchronises the host.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     All work is enqueued asynchronously on it, in order.
+ *   - Packed MXFP4: two E2M1 codes per byte, low nibble = even K index;
+ *     one E8M0 byte per 32 K values (value 2^(s-127), s = 255 is NaN).
+ *   - Rows are K-contiguous; *_row_stride arguments are in elements of the
+ *     tensor (bytes for uint8 tensors).  Packed/activation rows and their base
+ *     pointers must be 16-byte aligned.
+ *   - Every entry point returns MXFP4_OK (0) or an error class below and
+ *     leaves a message for mxfp4_last_error().  Argument errors are detected
+ *     before anything is enqueued.
+ */
+#ifndef MXFP4_GFX950_H_
+#define MXFP4_GFX950_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error classes; the Python layer raises the exception named beside each,
+ * matching the reference's conventions (soft:283-294, 317-329, 398-407). */
+enum {
+  MXFP4_OK = 0,
+  MXFP4_ERR_TYPE = 1,            /* TypeError: unsupported dtype */
+  MXFP4_ERR_VALUE = 2,           /* ValueError: shapes, K divisibility */
+  MXFP4_ERR_NOT_IMPLEMENTED = 3, /* NotImplementedError: swizzled scales */
+  MXFP4_ERR_RUNTIME = 4,         /* RuntimeError: unsupported metadata */
+  MXFP4_ERR_HIP = 5              /* RuntimeError: HIP launch/runtime failure */
+};
+
+/* Element types. */
+enum {
+  MXFP4_DT_F32 = 0,
+  MXFP4_DT_BF16 = 1,
+  MXFP4_DT_F16 = 2,
+  MXFP4_DT_U8 = 3, /* packed E2M1 pairs */
+  MXFP4_DT_I32 = 4,
+  MXFP4_DT_I64 = 5
+};
+
+/* Quantizer rounding modes for mxfp4_quant. */
+enum {
+  MXFP4_QUANT_TIES_AWAY = 0, /* the reference test quantizer, test:28-60 */
+  MXFP4_QUANT_RNE = 1        /* OCP MX: E = floor(log2 amax) - 2, E2M1 RNE */
+};
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* mxfp4_last_error(void);
+
+/* ABI version of this library (MXFP4_ABI_VERSION). */
+#define MXFP4_ABI_VERSION 1
+int mxfp4_abi_version(void);
+
+/*
+ * dequant_mxfp4(packed, block_scales, dtype) -- soft:277-307.
+ * packed u8 [rows, k/2], scales u8 [rows, k/32] -> out [rows, k] of out_dtype
+ * (F32, BF16 or F16), contiguous.  Bit-exact with the reference: the FP32
+ * product LUT[code] * 2^(s-127) rounded to out_dtype with RNE; s = 255 gives
+ * the canonical NaN (0x7FC00000 / 0x7FC0 / 0x7E00).  k % 32 == 0.
+ */
+int mxfp4_dequant(const uint8_t* packed, int64_t packed_row_stride, const uint8_t* scales,
+                  int64_t scale_row_stride, int64_t rows, int64_t k, void* out, int out_dtype,
+                  void* stream);
+
+/*
+ * linear_mxfp4_soft(x, packed, block_scales, bias) -- soft:310-376.
+ * x [m, k] (BF16 or F16, row stride x_row_stride elements), W packed u8
+ * [n, k/2], S u8 [n, k/32] (both contiguous) -> out [m, n] contiguous, same
+ * dtype as x:  out = x . dequant(W, S)^T (+ bias), FP32 accumulation, one
+ * rounding.  bias (optional, NULL for none) is [n] of x's dtype.
+ * k % 128 == 0 (soft:326-327).
+ */
+int mxfp4_linear_w4a16(const void* x, int x_dtype, int64_t m, int64_t k, int64_t x_row_stride,
+                       const uint8_t* packed, const uint8_t* scales, int64_t n, const void* bias,
+                       void* out, void* stream);
+
+/*
+ * Dense W4A4: both operands packed MXFP4, on gfx950's block-scaled MFMA
+ * (the packed-A semantics of aiter:206-214, 329-338 with one expert).
+ * a u8 [m, k/2], a_mx u8 [m, k/32], b u8 [n, k/2], b_mx u8 [n, k/32] (all
+ * contiguous) -> out [m, n] of out_dtype (BF16, F16 or F32).  k % 32 == 0.
+ */
+int mxfp4_linear_w4a4(const uint8_t* a, const uint8_t* a_mx, int64_t m, int64_t k,
+                      const uint8_t* b, const uint8_t* b_mx, int64_t n, void* out, int out_dtype,
+                      void* stream);
+
+/*
+ * Routing metadata on the device -- the format of vllm:119-146 (consumed as
+ * in soft:101-108).  topk_ids [num_routes] (I32 or I64; route r = token *
+ * top_k + slot) -> sorted_ids (route ids grouped by ascending expert,
+ * ascending inside an expert, each expert padded to block_m with the
+ * sentinel num_routes), expert_ids (one per block), num_post_padded[0] =
+ * number of entries used in sorted_ids.  Ids outside [0, num_experts) are
+ * dropped (their rows are left untouched by the GEMMs, as in soft:478-481).
+ * Deterministic.  Capacities come from mxfp4_moe_align_sizes; `workspace`
+ * must hold align_workspace_bytes bytes.
+ */
+int mxfp4_moe_align_sizes(int64_t num_routes, int num_experts, int block_m, int64_t* max_sorted,
+                          int64_t* max_blocks, int64_t* align_workspace_bytes);
+int mxfp4_moe_align(const void* topk_ids, int ids_dtype, int64_t num_routes, int num_experts,
+                    int block_m, int32_t* sorted_ids, int32_t* expert_ids,
+                    int32_t* num_post_padded, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+
+/*
+ * Routed grouped GEMM -- the compute of fused_moe_mxfp4_soft, soft:379-494,
+ * and of AITER's fused_moe_mxfp4, aiter:28-364.
+ *   a: activations [a_rows, k]: BF16/F16/F32 (a_dtype), or packed u8
+ *      [a_rows, k/2] with a_mx u8 [a_rows, k/32] (a_dtype = MXFP4_DT_U8).
+ *   b u8 [num_experts, n, k/2], b_mx u8 [num_experts, n, k/32], contiguous.
+ *   c: output rows indexed by route id, c + route * c_row_stride, of c_dtype
+ *      (BF16, F16 or F32; the compute type of soft:405-407).
+ *   For each block i < num_post_padded[0] / block_m with expert
+ *   e = expert_ids[i] and each route r = sorted_ids[i*block_m + j] <
+ *   num_valid:  c[r, :] = a[r / top_k] . dequant(b[e])^T * a_scale[0] *
+ *   b_scale[e] (* topk_weights[r] if mul_routed_weight), rounded once to
+ *   c_dtype.  Expert -1 writes zeros (aiter:156-172).  Rows not named by
+ *   the metadata are not written.  a_scale / b_scale may be NULL (= 1).
+ *   block_m % 16 == 0; k % 32 == 0; em = capacity of sorted_ids.
+ */
+int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
+                   const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,
+                   int64_t num_experts, int64_t n, int64_t k, void* c, int c_dtype,
+                   int64_t c_row_stride, const float* a_scale, const float* b_scale,
+                   const float* topk_weights, int mul_routed_weight, const int32_t* sorted_ids,
+                   const int32_t* expert_ids, const int32_t* num_post_padded, int64_t em,
+                   int block_m, int64_t num_valid, int top_k, void* stream);
+
+/*
+ * The vLLM MoE layer, vllm:233-265 (silu only):
+ *   gu = moe(x, w13)                  [m, top_k, 2*inter] rounded to x's dtype
+ *   h  = silu(gu[..., :inter]) * gu[..., inter:]   (rounded as the reference)
+ *   d  = moe(h, w2) * topk_weights    [m*top_k, hidden]
+ *   out = sum over top_k of d          [m, hidden], FP32 sum, one rounding
+ * x [m, hidden] BF16/F16 contiguous; w13 u8 [E, 2*inter, hidden/2],
+ * s13 u8 [E, 2*inter, hidden/32], w2 u8 [E, hidden, inter/2],
+ * s2 u8 [E, hidden, inter/32]; topk_weights F32 [m, top_k]; topk_ids I32/I64
+ * [m, top_k].  SiLU*mul is fused into the gate_up epilogue and the route
+ * weight into the down epilogue.  `workspace` must hold
+ * mxfp4_moe_layer_workspace_size bytes (routing metadata + intermediates).
+ */
+int mxfp4_moe_layer_workspace_size(int64_t m, int top_k, int num_experts, int64_t hidden,
+                                   int64_t inter, int64_t* bytes);
+int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hidden, const uint8_t* w13,
+                    const uint8_t* s13, const uint8_t* w2, const uint8_t* s2, int num_experts,
+                    int64_t inter, const float* topk_weights, const void* topk_ids, int ids_dtype,
+                    int top_k, void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * MXFP4 activation quantizer (the step before W4A4).  x [rows, k] (BF16,
+ * F16 or F32, row stride in elements) -> packed u8 [rows, k/2] and
+ * scales u8 [rows, k/32], contiguous.  mode MXFP4_QUANT_TIES_AWAY
+ * reproduces the reference test quantizer bit for bit (test:28-60);
+ * MXFP4_QUANT_RNE is the OCP MX rule.  k % 32 == 0.
+ */
+int mxfp4_quant(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t x_row_stride,
+                int mode, uint8_t* packed, uint8_t* scales, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXFP4_GFX950_H_ */

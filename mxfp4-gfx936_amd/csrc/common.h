@@ -1,0 +1,100 @@
+// Shared device helpers and host status plumbing for libmxfp4_gfx950.
+//
+// Formats (OCP MX v1.0, as used by the moe_op_mxfp4_soft operator surface):
+//   * weights/activations: E2M1 nibbles packed two per byte, the low nibble is
+//     the even K index;
+//   * one E8M0 byte per 32 consecutive K values, value 2^(s-127), s = 255 NaN.
+// gfx950 converts a byte of two E2M1 codes times an FP32 scale to two
+// bf16/fp16 values in one instruction (v_cvt_scalef32_pk_{bf16,f16}_fp4);
+// fed the scale 2^(s-127) (the FP32 subnormal 2^-127 for s = 0, a quiet NaN
+// for s = 255) it returns exactly the reference's dequantized value rounded to
+// bf16/fp16, for all 16 codes x 256 scales.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mxfp4_gfx950.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+namespace mx {
+
+// ---------------------------------------------------------------- host side
+// Thread-local message for the last failing call; see mxfp4_last_error().
+void set_error(const char* fmt, ...);
+int hip_status(hipError_t e, const char* what);  // 0 or MXFP4_ERR_HIP
+int launch_status(const char* what);             // checks hipGetLastError()
+
+// ---------------------------------------------------------------- device side
+
+// E8M0 byte -> the FP32 scale the converter expects.
+__device__ __forceinline__ float e8m0_scale(uint32_t s) {
+  uint32_t bits = s << 23;
+  bits = (s == 0u) ? 0x00400000u : bits;    // 2^-127 is an FP32 subnormal
+  bits = (s == 255u) ? 0x7FC00000u : bits;  // NaN scale -> NaN for every code
+  return __uint_as_float(bits);
+}
+
+// Eight E2M1 codes (one dword, low nibble first) times scale -> 8 x T.
+template <typename T>
+struct Decode;
+
+template <>
+struct Decode<__bf16> {
+  typedef bf16x8 vec8;
+  __device__ __forceinline__ static bf16x8 run(uint32_t p, float scale) {
+    bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, scale, 0);
+    bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, scale, 1);
+    bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, scale, 2);
+    bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, scale, 3);
+    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+  }
+};
+
+template <>
+struct Decode<_Float16> {
+  typedef f16x8 vec8;
+  __device__ __forceinline__ static f16x8 run(uint32_t p, float scale) {
+    f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(p, scale, 0);
+    f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(p, scale, 1);
+    f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(p, scale, 2);
+    f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(p, scale, 3);
+    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+  }
+};
+
+// 16x16x32 MFMA, FP32 accumulate.  Lane l holds A[l%16][(l/16)*8 + 0..7],
+// B[(l/16)*8 + 0..7][l%16]; the result lane l holds D[(l/16)*4 + i][l%16].
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Scalar conversions with round-to-nearest-even.
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ __bf16 from_f32<__bf16>(float v) { return (__bf16)v; }
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return (_Float16)v; }
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) { return (float)v; }
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+}  // namespace mx

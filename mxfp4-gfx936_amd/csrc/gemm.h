@@ -1,0 +1,88 @@
+// Arguments shared by the routed / dense MXFP4 GEMM kernels.
+//
+// One argument block describes both the dense linear (no routing metadata:
+// output row i reads activation row i) and the routed grouped GEMM of the
+// MoE operator (soft:65-173 / aiter:28-364 semantics): padded position p of
+// `sorted_ids` names route r = sorted_ids[p]; r >= num_valid is padding;
+// the block of `block_m` positions containing p belongs to expert
+// expert_ids[p / block_m] (-1 = not on this device: write zeros); the
+// activation row is r / top_k and the output row is r.
+#pragma once
+
+#include "common.h"
+
+namespace mx {
+
+enum Epilogue {
+  EPI_STORE = 0,     // c = T(acc * alpha [* route_w] [+ bias])
+  EPI_SILU_MUL = 1,  // gate/up column pairs -> h = silu(g) * u, rounded like vllm:249-252
+};
+
+struct GemmArgs {
+  const void* a;        // activations (T) or packed u8
+  const uint8_t* a_mx;  // packed A scales [a_rows, k/32] (W4A4 only)
+  int64_t lda;          // A row stride, elements (bytes for packed A)
+  int64_t lda_mx;       // A scale row stride, bytes
+  const uint8_t* b;     // packed weights, expert-major
+  const uint8_t* bs;    // E8M0 weight scales
+  int64_t b_e, b_n;     // byte strides: expert, row
+  int64_t bs_e, bs_n;
+  void* c;
+  int64_t ldc;  // output row stride, elements
+  const int32_t* sorted_ids;       // nullptr => dense rows
+  const int32_t* expert_ids;
+  const int32_t* num_post_padded;  // device scalar
+  const float* a_scale;            // [1] or nullptr
+  const float* b_scale;            // [E] or nullptr
+  const float* route_w;            // [num_valid] or nullptr
+  const void* bias;                // [n] of T or nullptr (dense)
+  int64_t m;          // dense: rows; routed: capacity of sorted_ids (em)
+  int64_t num_valid;  // routed: route count (sentinel >= num_valid)
+  int32_t n;          // output columns
+  int32_t k;          // reduction length (multiple of 32)
+  int32_t top_k;      // activation row = route / top_k
+  int32_t block_m;    // rows per expert block in sorted_ids
+  int32_t inter;      // SiLU epilogue: row offset of the `up` half in B
+};
+
+// Per-row routing lookup used by every kernel.
+struct RowInfo {
+  int64_t out_row;  // output row (route id or dense row)
+  int64_t a_row;    // activation row
+  bool valid;
+};
+
+__device__ __forceinline__ RowInfo row_info(const GemmArgs& g, int64_t pos) {
+  RowInfo ri;
+  if (g.sorted_ids == nullptr) {
+    ri.valid = pos < g.m;
+    ri.out_row = pos;
+    ri.a_row = pos;
+  } else {
+    const int32_t r = g.sorted_ids[pos];
+    ri.valid = (r >= 0) && (r < g.num_valid);
+    ri.out_row = r;
+    ri.a_row = ri.valid ? (r / g.top_k) : 0;
+  }
+  return ri;
+}
+
+// Number of padded rows in use (routed: read from the device scalar).
+__device__ __forceinline__ int64_t rows_in_use(const GemmArgs& g) {
+  if (g.sorted_ids == nullptr) return g.m;
+  int64_t npp = *g.num_post_padded;
+  return npp < g.m ? npp : g.m;
+}
+
+__device__ __forceinline__ float scalar_alpha(const GemmArgs& g, int expert) {
+  float a = g.a_scale ? g.a_scale[0] : 1.0f;
+  if (g.b_scale) a *= g.b_scale[expert];
+  return a;
+}
+
+// Host-side launchers (gemm_w4a16.hip, gemm_w4a4.hip).
+int launch_w4a16(const GemmArgs& g, int dtype, int epi, hipStream_t st);
+int launch_w4a4(const GemmArgs& g, int out_dtype, hipStream_t st);
+int launch_f32_reference(const GemmArgs& g, int a_dtype, hipStream_t st);
+
+}  // namespace mx

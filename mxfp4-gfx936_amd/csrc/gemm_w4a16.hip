@@ -1,0 +1,460 @@
+// W4A16 GEMM kernels: BF16/FP16 activations x packed MXFP4 weights, FP32
+// accumulation on the 16x16x32 MFMA, E2M1 decode in registers.
+//
+// Two shapes of kernel serve the dense linear (soft:310-376) and the routed
+// grouped GEMM (soft:65-173, 379-494):
+//
+// * skinny (decode, <= 32 rows per tile): a workgroup owns 16 output columns
+//   and one 16/32-row block; its waves split K.  Each lane streams 16 bytes
+//   of packed weights (32 K values = exactly one E8M0 block) per step straight
+//   from HBM into registers -- per row 4 lanes cover 64 contiguous bytes --
+//   decodes them to 4 MFMA B fragments, and reuses them for up to two 16-row
+//   A blocks.  The waves' partial tiles are reduced through LDS in a fixed
+//   order, so results are bitwise repeatable (no atomics).
+//
+// * tiled (prefill): 256-thread workgroups own a BM x BN tile; each 64-deep K
+//   stage moves the A tile (BM x 64 bf16) and the packed B tile (BN x 32 B +
+//   2 scale bytes per row) global -> registers -> LDS, double buffered with
+//   one barrier per stage; waves (2 x 2) read MFMA fragments from LDS and
+//   decode B fragments in registers right before the MFMA.  The packed B
+//   tile is 4x smaller than a bf16 one, so LDS traffic is dominated by A.
+//
+// The SiLU*mul epilogue (vllm:249-252) pairs gate column j with up column
+// inter + j inside the same lane, so the gate_up GEMM writes h directly.
+#include "gemm.h"
+
+namespace mx {
+namespace {
+
+template <typename T>
+struct V8Of;
+template <>
+struct V8Of<__bf16> {
+  typedef bf16x8 type;
+};
+template <>
+struct V8Of<_Float16> {
+  typedef f16x8 type;
+};
+
+template <typename V>
+__device__ __forceinline__ V zero_v8() {
+  return __builtin_bit_cast(V, i32x4{0, 0, 0, 0});
+}
+
+// Epilogue for one output element.
+template <typename T, int EPI>
+__device__ __forceinline__ void store_out(const GemmArgs& g, const RowInfo& r, int col,
+                                          float alpha, float v0, float v1) {
+  T* cp = static_cast<T*>(g.c) + r.out_row * g.ldc + col;
+  if (EPI == EPI_STORE) {
+    float o = v0 * alpha;
+    if (g.route_w) o *= g.route_w[r.out_row];
+    if (g.bias) o += to_f32(static_cast<const T*>(g.bias)[col]);
+    *cp = from_f32<T>(o);
+  } else {
+    // vllm:249-252 on tensors of T: gate_up rounded to T, silu evaluated in
+    // FP32 and rounded to T, the product rounded to T.
+    const T gb = from_f32<T>(v0 * alpha);
+    const T ub = from_f32<T>(v1 * alpha);
+    const T sb = from_f32<T>(silu_f32(to_f32(gb)));
+    *cp = from_f32<T>(to_f32(sb) * to_f32(ub));
+  }
+}
+
+// ---------------------------------------------------------------- skinny
+template <typename T, int RB, int NW, int EPI>
+__global__ __launch_bounds__(NW * 64) void w4a16_skinny(GemmArgs g) {
+  typedef typename V8Of<T>::type V8;
+  constexpr int CB = (EPI == EPI_SILU_MUL) ? 2 : 1;
+  __shared__ f32x4 red[NW][RB * CB][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15;
+  const int grp = lane >> 4;
+  const int64_t pos0 = (int64_t)blockIdx.y * (16 * RB);
+  if (pos0 >= rows_in_use(g)) return;
+  const int expert = g.sorted_ids ? g.expert_ids[pos0 / g.block_m] : 0;
+  const int n0 = blockIdx.x * 16;
+
+  f32x4 acc[RB][CB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (expert >= 0) {
+    const int col = n0 + c16;
+    const bool col_ok = col < g.n;
+    const uint8_t* bp[CB];
+    const uint8_t* sp[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int64_t brow = (cb == 0 ? 0 : g.inter) + (col_ok ? col : 0);
+      bp[cb] = g.b + expert * g.b_e + brow * g.b_n;
+      sp[cb] = g.bs + expert * g.bs_e + brow * g.bs_n;
+    }
+    const T* ap[RB];
+    bool a_ok[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const RowInfo ri = row_info(g, pos0 + rb * 16 + c16);
+      a_ok[rb] = ri.valid;
+      ap[rb] = static_cast<const T*>(g.a) + ri.a_row * g.lda;
+    }
+    const int nunits = (g.k + 127) >> 7;
+    for (int u = wave; u < nunits; u += NW) {
+      const int k0 = u * 128 + grp * 32;
+      const bool k_ok = k0 < g.k;
+      i32x4 braw[CB];
+      float bsc[CB];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        if (col_ok && k_ok) {
+          braw[cb] = *reinterpret_cast<const i32x4*>(bp[cb] + (k0 >> 1));
+          bsc[cb] = e8m0_scale(sp[cb][k0 >> 5]);
+        } else {
+          braw[cb] = i32x4{0, 0, 0, 0};
+          bsc[cb] = 1.0f;
+        }
+      }
+      V8 af[RB][4];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        if (a_ok[rb] && k_ok) {
+          const V8* src = reinterpret_cast<const V8*>(ap[rb] + k0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) af[rb][j] = src[j];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) af[rb][j] = zero_v8<V8>();
+        }
+      }
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const V8 bf = Decode<T>::run((uint32_t)braw[cb][j], bsc[cb]);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) acc[rb][cb] = mfma16(af[rb][j], bf, acc[rb][cb]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) red[wave][rb * CB + cb][lane] = acc[rb][cb];
+  __syncthreads();
+
+  const float alpha = expert >= 0 ? scalar_alpha(g, expert) : 0.f;
+  for (int idx = threadIdx.x; idx < RB * 256; idx += NW * 64) {
+    const int rb = idx >> 8;
+    const int l = (idx >> 2) & 63;
+    const int i = idx & 3;
+    const int col = n0 + (l & 15);
+    const RowInfo r = row_info(g, pos0 + rb * 16 + (l >> 4) * 4 + i);
+    if (!r.valid || col >= g.n) continue;
+    if (expert < 0) {
+      static_cast<T*>(g.c)[r.out_row * g.ldc + col] = from_f32<T>(0.f);
+      continue;
+    }
+    float v[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) s += red[w][rb * CB + cb][l][i];
+      v[cb] = s;
+    }
+    store_out<T, EPI>(g, r, col, alpha, v[0], v[CB - 1]);
+  }
+}
+
+// ---------------------------------------------------------------- tiled
+template <typename T, int FM, int FN, int EPI>
+__global__ __launch_bounds__(256) void w4a16_tiled(GemmArgs g) {
+  typedef typename V8Of<T>::type V8;
+  constexpr int WGM = 2, WGN = 2;
+  constexpr int BM = WGM * FM * 16;  // tile rows
+  constexpr int BN = WGN * FN * 16;  // B-tile rows (weight rows)
+  constexpr int BK = 64;
+  constexpr int A_LD = BK + 8;  // elements; 144-byte rows keep b128 reads conflict-free
+  constexpr int B_LD = 40;      // bytes; 10-dword rows spread 16 rows over distinct banks
+  constexpr int A_PER = BM * 8 / 256;
+  constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
+  static_assert(A_PER >= 1 && BN == 128, "tile config");
+  static_assert(EPI != EPI_SILU_MUL || FN % 2 == 0, "SiLU pairs need even FN");
+
+  __shared__ __attribute__((aligned(16))) T As[2][BM][A_LD];
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN][B_LD];
+  __shared__ uint8_t Ss[2][BN][2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int c16 = lane & 15;
+  const int grp = lane >> 4;
+
+  const int64_t pos0 = (int64_t)blockIdx.y * BM;
+  if (pos0 >= rows_in_use(g)) return;
+  const int expert = g.sorted_ids ? g.expert_ids[pos0 / g.block_m] : 0;
+  const int ncol0 = blockIdx.x * OUT_COLS;
+
+  if (expert < 0) {  // aiter:156-172: expert not on this device -> zeros
+    for (int idx = tid; idx < BM * OUT_COLS; idx += 256) {
+      const int r = idx / OUT_COLS, cc = idx % OUT_COLS;
+      const RowInfo ri = row_info(g, pos0 + r);
+      if (ri.valid && ncol0 + cc < g.n)
+        static_cast<T*>(g.c)[ri.out_row * g.ldc + ncol0 + cc] = from_f32<T>(0.f);
+    }
+    return;
+  }
+
+  // ---- per-thread global load assignments
+  const T* a_src[A_PER];
+  int a_r[A_PER], a_kc[A_PER];
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i) {
+    const int c = tid + i * 256;
+    a_r[i] = c >> 3;
+    a_kc[i] = c & 7;
+    const RowInfo ri = row_info(g, pos0 + a_r[i]);
+    a_src[i] = ri.valid ? static_cast<const T*>(g.a) + ri.a_row * g.lda : nullptr;
+  }
+  // B tile row -> weight row
+  auto weight_row = [&](int i, bool& ok) -> int64_t {
+    int orow;
+    int64_t grow;
+    if (EPI == EPI_SILU_MUL) {
+      const int cbk = i >> 4;
+      orow = ncol0 + (cbk >> 1) * 16 + (i & 15);
+      grow = (cbk & 1 ? g.inter : 0) + orow;
+    } else {
+      orow = ncol0 + i;
+      grow = orow;
+    }
+    ok = orow < g.n;
+    return grow;
+  };
+  const int b_r = tid >> 1, b_h = tid & 1;  // 256 threads = BN rows x 2 halves
+  bool b_ok;
+  const int64_t b_grow = weight_row(b_r, b_ok);
+  const uint8_t* b_src = b_ok ? g.b + expert * g.b_e + b_grow * g.b_n : nullptr;
+  const uint8_t* s_src = nullptr;
+  if (tid < BN) {
+    bool ok;
+    const int64_t grow = weight_row(tid, ok);
+    s_src = ok ? g.bs + expert * g.bs_e + grow * g.bs_n : nullptr;
+  }
+
+  i32x4 areg[A_PER];
+  i32x4 breg;
+  uint8_t sreg0 = 127, sreg1 = 127;
+
+  auto load_global = [&](int kt) {
+    const int kbase = kt * BK;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int k = kbase + a_kc[i] * 8;
+      areg[i] = (a_src[i] && k < g.k) ? *reinterpret_cast<const i32x4*>(a_src[i] + k)
+                                       : i32x4{0, 0, 0, 0};
+    }
+    const int kb = kbase + b_h * 32;
+    breg = (b_src && kb < g.k) ? *reinterpret_cast<const i32x4*>(b_src + (kb >> 1))
+                               : i32x4{0, 0, 0, 0};
+    if (tid < BN) {
+      sreg0 = (s_src && kbase < g.k) ? s_src[kbase >> 5] : (uint8_t)127;
+      sreg1 = (s_src && kbase + 32 < g.k) ? s_src[(kbase >> 5) + 1] : (uint8_t)127;
+    }
+  };
+  auto store_lds = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i)
+      *reinterpret_cast<i32x4*>(&As[buf][a_r[i]][a_kc[i] * 8]) = areg[i];
+    int64_t* bdst = reinterpret_cast<int64_t*>(&Bs[buf][b_r][b_h * 16]);
+    const i32x4 bv = breg;
+    bdst[0] = ((int64_t)(uint32_t)bv[1] << 32) | (uint32_t)bv[0];
+    bdst[1] = ((int64_t)(uint32_t)bv[3] << 32) | (uint32_t)bv[2];
+    if (tid < BN) {
+      Ss[buf][tid][0] = sreg0;
+      Ss[buf][tid][1] = sreg1;
+    }
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (g.k + BK - 1) / BK;
+  load_global(0);
+  store_lds(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_global(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      V8 af[FM];
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+        af[fm] = *reinterpret_cast<const V8*>(
+            &As[buf][wm * FM * 16 + fm * 16 + c16][ks * 32 + grp * 8]);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int br = wn * FN * 16 + fn * 16 + c16;
+        const uint32_t raw = *reinterpret_cast<const uint32_t*>(&Bs[buf][br][ks * 16 + grp * 4]);
+        const V8 bf = Decode<T>::run(raw, e8m0_scale(Ss[buf][br][ks]));
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) acc[fm][fn] = mfma16(af[fm], bf, acc[fm][fn]);
+      }
+    }
+    if (kt + 1 < nk) store_lds(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue
+  const float alpha = scalar_alpha(g, expert);
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const RowInfo r = row_info(g, pos0 + wm * FM * 16 + fm * 16 + grp * 4 + i);
+      if (!r.valid) continue;
+      if (EPI == EPI_SILU_MUL) {
+#pragma unroll
+        for (int fn = 0; fn < FN; fn += 2) {
+          const int col = ncol0 + ((wn * FN + fn) >> 1) * 16 + c16;
+          if (col < g.n) store_out<T, EPI>(g, r, col, alpha, acc[fm][fn][i], acc[fm][fn + 1][i]);
+        }
+      } else {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int col = ncol0 + wn * FN * 16 + fn * 16 + c16;
+          if (col < g.n) store_out<T, EPI>(g, r, col, alpha, acc[fm][fn][i], 0.f);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- FP32 compute
+// soft:405-407 allows C (and so the compute dtype) to be FP32; the reference
+// then runs an FP32 GEMM.  Weights decode exactly to FP32; activations are
+// read as TA and widened.  One thread per output, sequential FMA over K.
+template <typename TA>
+__global__ __launch_bounds__(256) void f32_gemm(GemmArgs g) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  const int64_t used = rows_in_use(g);
+  for (int64_t pos = blockIdx.y; pos < used; pos += gridDim.y) {
+    const RowInfo r = row_info(g, pos);
+    if (!r.valid || col >= g.n) continue;
+    const int expert = g.sorted_ids ? g.expert_ids[pos / g.block_m] : 0;
+    float* cp = static_cast<float*>(g.c) + r.out_row * g.ldc + col;
+    if (expert < 0) {
+      *cp = 0.f;
+      continue;
+    }
+    const uint8_t* bp = g.b + expert * g.b_e + (int64_t)col * g.b_n;
+    const uint8_t* sp = g.bs + expert * g.bs_e + (int64_t)col * g.bs_n;
+    const TA* ap = static_cast<const TA*>(g.a) + r.a_row * g.lda;
+    float acc = 0.f;
+    for (int k0 = 0; k0 < g.k; k0 += 8) {
+      const bf16x8 w = Decode<__bf16>::run(*reinterpret_cast<const uint32_t*>(bp + (k0 >> 1)),
+                                           e8m0_scale(sp[k0 >> 5]));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf((float)ap[k0 + j], (float)w[j], acc);
+    }
+    float o = acc * scalar_alpha(g, expert);
+    if (g.route_w) o *= g.route_w[r.out_row];
+    *cp = o;
+  }
+}
+
+// ---------------------------------------------------------------- dispatch
+template <typename T, int EPI>
+int launch_typed(const GemmArgs& g, hipStream_t st) {
+  const int64_t cap = g.m;  // dense rows or sorted capacity
+  const bool routed = g.sorted_ids != nullptr;
+  const int out_cols = g.n;
+  // skinny for 16/32-row blocks (and any routed block size that is not a
+  // multiple of 32); tiled otherwise.
+  int skinny_rb = 0;
+  if (routed) {
+    if (g.block_m % 32 != 0) skinny_rb = 1;
+    else if (g.block_m == 32) skinny_rb = 2;
+  } else if (cap <= 32) {
+    skinny_rb = cap <= 16 ? 1 : 2;
+  }
+  if (skinny_rb) {
+    const int rb = skinny_rb;
+    const int64_t gy = (cap + 16 * rb - 1) / (16 * rb);
+    if (gy > 65535) {
+      set_error("w4a16: too many row blocks (%lld)", (long long)gy);
+      return MXFP4_ERR_VALUE;
+    }
+    dim3 grid((out_cols + 15) / 16, (unsigned)(gy > 0 ? gy : 1));
+    if (rb == 1)
+      w4a16_skinny<T, 1, 8, EPI><<<grid, 512, 0, st>>>(g);
+    else
+      w4a16_skinny<T, 2, 8, EPI><<<grid, 512, 0, st>>>(g);
+    return launch_status("w4a16 skinny launch");
+  }
+  // tiled: BM must divide block_m (routed); pick the largest BM that still
+  // gives >= 512 workgroups, else the smallest.
+  const int tile_cols = (EPI == EPI_SILU_MUL) ? 64 : 128;
+  const int64_t ntiles = (out_cols + tile_cols - 1) / tile_cols;
+  int bm = 32;
+  const int cands[3] = {128, 64, 32};
+  for (int i = 0; i < 3; ++i) {
+    const int c = cands[i];
+    if (routed && (g.block_m % c) != 0) continue;
+    if (((cap + c - 1) / c) * ntiles >= 512) {
+      bm = c;
+      break;
+    }
+  }
+  dim3 grid((unsigned)ntiles, (unsigned)((cap + bm - 1) / bm));
+  if (grid.y > 65535u) {
+    set_error("w4a16: too many row tiles (%lld)", (long long)grid.y);
+    return MXFP4_ERR_VALUE;
+  }
+  switch (bm) {
+    case 128: w4a16_tiled<T, 4, 4, EPI><<<grid, 256, 0, st>>>(g); break;
+    case 64: w4a16_tiled<T, 2, 4, EPI><<<grid, 256, 0, st>>>(g); break;
+    default: w4a16_tiled<T, 1, 4, EPI><<<grid, 256, 0, st>>>(g); break;
+  }
+  return launch_status("w4a16 tiled launch");
+}
+
+}  // namespace
+
+int launch_w4a16(const GemmArgs& g, int dtype, int epi, hipStream_t st) {
+  if (dtype == MXFP4_DT_BF16)
+    return epi == EPI_STORE ? launch_typed<__bf16, EPI_STORE>(g, st)
+                            : launch_typed<__bf16, EPI_SILU_MUL>(g, st);
+  if (dtype == MXFP4_DT_F16)
+    return epi == EPI_STORE ? launch_typed<_Float16, EPI_STORE>(g, st)
+                            : launch_typed<_Float16, EPI_SILU_MUL>(g, st);
+  set_error("w4a16: unsupported compute dtype %d", dtype);
+  return MXFP4_ERR_TYPE;
+}
+
+int launch_f32_reference(const GemmArgs& g, int a_dtype, hipStream_t st) {
+  const int64_t cap = g.m;
+  dim3 grid((g.n + 255) / 256, (unsigned)(cap < 65535 ? (cap > 0 ? cap : 1) : 65535));
+  switch (a_dtype) {
+    case MXFP4_DT_F32: f32_gemm<float><<<grid, 256, 0, st>>>(g); break;
+    case MXFP4_DT_BF16: f32_gemm<__bf16><<<grid, 256, 0, st>>>(g); break;
+    case MXFP4_DT_F16: f32_gemm<_Float16><<<grid, 256, 0, st>>>(g); break;
+    default: set_error("f32 gemm: unsupported activation dtype %d", a_dtype); return MXFP4_ERR_TYPE;
+  }
+  return launch_status("f32 gemm launch");
+}
+
+}  // namespace mx

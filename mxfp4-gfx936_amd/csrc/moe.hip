@@ -1,0 +1,563 @@
+// Routed MoE on the device: routing metadata, the grouped-GEMM entry points,
+// the top-k combine, and the whole vLLM MoE layer (vllm:233-265).
+//
+// Routing (the format of vllm:119-146, consumed as soft:101-108) is built
+// without any host synchronisation in three deterministic passes over
+// 1024-route chunks:
+//   count  -- per-chunk expert histogram (LDS atomics; counts only);
+//   scan   -- one workgroup turns the histograms into, for every (chunk,
+//             expert), the absolute position of that chunk's first route of
+//             that expert, pads every expert to block_m, writes expert_ids,
+//             the sentinel padding and num_tokens_post_padded;
+//   place  -- each chunk places its routes in route order: the rank of a
+//             route among earlier same-expert routes of its wave comes from
+//             ballots over the expert-id bits, across waves from a small
+//             per-wave count table in LDS.
+// The result is identical to the host loop of vllm:119-146 (ascending
+// experts, ascending route ids inside an expert) for ids in [0, E); other ids
+// are dropped, leaving those rows untouched (soft:476-481: they stay zero).
+#include "gemm.h"
+
+namespace mx {
+namespace {
+
+constexpr int kChunk = 1024;  // routes per count/place workgroup
+constexpr int kMaxExperts = 1024;
+
+template <typename TI>
+__global__ __launch_bounds__(256) void align_count(const TI* __restrict__ ids, int64_t n,
+                                                   int num_experts,
+                                                   int32_t* __restrict__ counts) {
+  __shared__ int hist[kMaxExperts];
+  for (int e = threadIdx.x; e < num_experts; e += 256) hist[e] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kChunk;
+  for (int i = 0; i < kChunk / 256; ++i) {
+    const int64_t r = base + i * 256 + threadIdx.x;
+    if (r < n) {
+      const int64_t e = (int64_t)ids[r];
+      if (e >= 0 && e < num_experts) atomicAdd(&hist[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < num_experts; e += 256)
+    counts[(int64_t)blockIdx.x * num_experts + e] = hist[e];
+}
+
+__global__ __launch_bounds__(1024) void align_scan(int32_t* __restrict__ counts, int nchunks,
+                                                   int num_experts, int block_m, int64_t n,
+                                                   int32_t* __restrict__ sorted_ids,
+                                                   int32_t* __restrict__ expert_ids,
+                                                   int32_t* __restrict__ num_post_padded) {
+  __shared__ int scan[kMaxExperts];
+  const int e = threadIdx.x;
+  int total = 0;
+  if (e < num_experts) {
+    for (int b = 0; b < nchunks; ++b) {
+      const int64_t idx = (int64_t)b * num_experts + e;
+      const int c = counts[idx];
+      counts[idx] = total;  // exclusive prefix within the expert
+      total += c;
+    }
+  }
+  const int padded = ((total + block_m - 1) / block_m) * block_m;
+  scan[e] = (e < num_experts) ? padded : 0;
+  __syncthreads();
+  // Hillis-Steele inclusive scan over 1024 entries
+  for (int off = 1; off < kMaxExperts; off <<= 1) {
+    const int v = (e >= off) ? scan[e - off] : 0;
+    __syncthreads();
+    scan[e] += v;
+    __syncthreads();
+  }
+  const int start = scan[e] - padded;  // exclusive
+  if (e < num_experts) {
+    for (int b = 0; b < nchunks; ++b) counts[(int64_t)b * num_experts + e] += start;
+    for (int blk = start / block_m; blk < (start + padded) / block_m; ++blk) expert_ids[blk] = e;
+    for (int p = start + total; p < start + padded; ++p) sorted_ids[p] = (int32_t)n;
+  }
+  if (e == kMaxExperts - 1) num_post_padded[0] = scan[e];
+}
+
+template <typename TI>
+__global__ __launch_bounds__(256) void align_place(const TI* __restrict__ ids, int64_t n,
+                                                   int num_experts, int id_bits,
+                                                   const int32_t* __restrict__ starts,
+                                                   int32_t* __restrict__ sorted_ids) {
+  __shared__ int cursor[kMaxExperts];
+  __shared__ int wcnt[4][kMaxExperts];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  for (int e = tid; e < num_experts; e += 256) {
+    cursor[e] = starts[(int64_t)blockIdx.x * num_experts + e];
+    wcnt[0][e] = wcnt[1][e] = wcnt[2][e] = wcnt[3][e] = 0;
+  }
+  __syncthreads();
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int64_t base = (int64_t)blockIdx.x * kChunk;
+  for (int it = 0; it < kChunk / 256; ++it) {
+    const int64_t r = base + it * 256 + tid;
+    int64_t e64 = -1;
+    if (r < n) e64 = (int64_t)ids[r];
+    const bool valid = e64 >= 0 && e64 < num_experts;
+    const int e = valid ? (int)e64 : 0;
+    uint64_t same = __ballot(valid);
+    for (int bit = 0; bit < id_bits; ++bit) {
+      const bool b = (e >> bit) & 1;
+      const uint64_t bal = __ballot(b);
+      same &= b ? bal : ~bal;
+    }
+    const int rank = __popcll(same & lt_mask);
+    if (valid && rank == 0) wcnt[wave][e] = __popcll(same);
+    __syncthreads();
+    if (valid) {
+      int before = cursor[e] + rank;
+      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
+      sorted_ids[before] = (int32_t)r;
+    }
+    __syncthreads();
+    for (int x = tid; x < num_experts; x += 256) {
+      cursor[x] += wcnt[0][x] + wcnt[1][x] + wcnt[2][x] + wcnt[3][x];
+      wcnt[0][x] = wcnt[1][x] = wcnt[2][x] = wcnt[3][x] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+// out[t, :] = sum over slots s of d[t * top_k + s, :] (FP32, slot order),
+// skipping slots whose expert id is outside [0, E) (their rows are zero in
+// the reference, soft:476).  vllm:263-265.
+template <typename T, typename TI>
+__global__ __launch_bounds__(256) void topk_sum(const T* __restrict__ d, const TI* __restrict__ ids,
+                                                int64_t m, int top_k, int64_t hidden,
+                                                int num_experts, T* __restrict__ out) {
+  typedef typename Decode<T>::vec8 V8;
+  const int64_t vecs = hidden >> 3;
+  const int64_t total = m * vecs;
+  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < total;
+       u += (int64_t)gridDim.x * 256) {
+    const int64_t t = u / vecs;
+    const int64_t c = (u - t * vecs) * 8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < top_k; ++s) {
+      const int64_t e = (int64_t)ids[t * top_k + s];
+      if (e < 0 || e >= num_experts) continue;
+      const V8 v = *reinterpret_cast<const V8*>(d + (t * top_k + s) * hidden + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += (float)v[j];
+    }
+    V8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = from_f32<T>(acc[j]);
+    *reinterpret_cast<V8*>(out + t * hidden + c) = o;
+  }
+}
+
+int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+void align_capacity(int64_t n, int num_experts, int block_m, int64_t* max_sorted,
+                    int64_t* max_blocks, int64_t* nchunks) {
+  const int64_t busy = n < num_experts ? n : num_experts;
+  const int64_t cap = round_up(n + busy * (block_m - 1), block_m);
+  *max_sorted = cap > 0 ? cap : block_m;
+  *max_blocks = *max_sorted / block_m;
+  *nchunks = (n + kChunk - 1) / kChunk;
+}
+
+int check_align_args(int64_t n, int num_experts, int block_m, int ids_dtype) {
+  if (ids_dtype != MXFP4_DT_I32 && ids_dtype != MXFP4_DT_I64) {
+    set_error("topk_ids must be int32 or int64");
+    return MXFP4_ERR_TYPE;
+  }
+  if (n < 0 || num_experts < 1 || num_experts > kMaxExperts || block_m < 16 || block_m % 16 ||
+      n > (int64_t)0x3FFFFFFF) {
+    set_error("routing: unsupported sizes (routes %lld, experts %d, block_m %d)", (long long)n,
+              num_experts, block_m);
+    return MXFP4_ERR_VALUE;
+  }
+  return MXFP4_OK;
+}
+
+template <typename TI>
+int launch_align(const TI* ids, int64_t n, int num_experts, int block_m, int32_t* sorted_ids,
+                 int32_t* expert_ids, int32_t* npp, int32_t* counts, int64_t nchunks,
+                 hipStream_t st) {
+  int id_bits = 0;
+  while ((1 << id_bits) < num_experts) ++id_bits;
+  if (nchunks > 0) {
+    align_count<TI><<<(unsigned)nchunks, 256, 0, st>>>(ids, n, num_experts, counts);
+    int rc = launch_status("align count launch");
+    if (rc) return rc;
+  }
+  align_scan<<<1, kMaxExperts, 0, st>>>(counts, (int)nchunks, num_experts, block_m, n, sorted_ids,
+                                        expert_ids, npp);
+  int rc = launch_status("align scan launch");
+  if (rc) return rc;
+  if (nchunks > 0) {
+    align_place<TI><<<(unsigned)nchunks, 256, 0, st>>>(ids, n, num_experts, id_bits, counts,
+                                                       sorted_ids);
+    rc = launch_status("align place launch");
+  }
+  return rc;
+}
+
+int do_align(const void* ids, int ids_dtype, int64_t n, int num_experts, int block_m,
+             int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, int32_t* counts,
+             int64_t nchunks, hipStream_t st) {
+  if (ids_dtype == MXFP4_DT_I32)
+    return launch_align(static_cast<const int32_t*>(ids), n, num_experts, block_m, sorted_ids,
+                        expert_ids, npp, counts, nchunks, st);
+  return launch_align(static_cast<const int64_t*>(ids), n, num_experts, block_m, sorted_ids,
+                      expert_ids, npp, counts, nchunks, st);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int dispatch_gemm(const GemmArgs& g, int a_dtype, int c_dtype, int epi, hipStream_t st) {
+  if (a_dtype == MXFP4_DT_U8) {
+    if (epi != EPI_STORE) {
+      set_error("packed activations support the plain epilogue only");
+      return MXFP4_ERR_VALUE;
+    }
+    return launch_w4a4(g, c_dtype, st);
+  }
+  if (c_dtype == MXFP4_DT_F32) {
+    if (epi != EPI_STORE) {
+      set_error("the FP32 compute path supports the plain epilogue only");
+      return MXFP4_ERR_TYPE;
+    }
+    return launch_f32_reference(g, a_dtype, st);
+  }
+  if (a_dtype != c_dtype) {
+    set_error("activation dtype %d must equal the compute dtype %d", a_dtype, c_dtype);
+    return MXFP4_ERR_TYPE;
+  }
+  return launch_w4a16(g, c_dtype, epi, st);
+}
+
+int64_t elem_size(int dt) {
+  switch (dt) {
+    case MXFP4_DT_F32: case MXFP4_DT_I32: return 4;
+    case MXFP4_DT_BF16: case MXFP4_DT_F16: return 2;
+    case MXFP4_DT_I64: return 8;
+    default: return 1;
+  }
+}
+
+struct LayerPlan {
+  int block_m;
+  int64_t routes, max_sorted, max_blocks, nchunks;
+  int64_t off_counts, off_sorted, off_experts, off_npp, off_h, off_d, total;
+};
+
+LayerPlan plan_layer(int64_t m, int top_k, int num_experts, int64_t hidden, int64_t inter,
+                     int64_t esize) {
+  LayerPlan p;
+  p.routes = m * top_k;
+  const double avg = (double)p.routes / (double)num_experts;
+  p.block_m = avg <= 8.0 ? 16 : (avg <= 20.0 ? 32 : (avg <= 80.0 ? 64 : 128));
+  align_capacity(p.routes, num_experts, p.block_m, &p.max_sorted, &p.max_blocks, &p.nchunks);
+  int64_t off = 0;
+  p.off_counts = off; off = round_up(off + (p.nchunks > 0 ? p.nchunks : 1) * num_experts * 4, 256);
+  p.off_sorted = off; off = round_up(off + p.max_sorted * 4, 256);
+  p.off_experts = off; off = round_up(off + p.max_blocks * 4, 256);
+  p.off_npp = off; off = round_up(off + 4, 256);
+  p.off_h = off; off = round_up(off + p.routes * inter * esize, 256);
+  p.off_d = off; off = round_up(off + p.routes * hidden * esize, 256);
+  p.total = off;
+  return p;
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mxfp4_moe_align_sizes(int64_t num_routes, int num_experts, int block_m,
+                                     int64_t* max_sorted, int64_t* max_blocks,
+                                     int64_t* align_workspace_bytes) {
+  int rc = check_align_args(num_routes, num_experts, block_m, MXFP4_DT_I64);
+  if (rc) return rc;
+  int64_t nchunks;
+  align_capacity(num_routes, num_experts, block_m, max_sorted, max_blocks, &nchunks);
+  *align_workspace_bytes = (nchunks > 0 ? nchunks : 1) * num_experts * 4;
+  return MXFP4_OK;
+}
+
+extern "C" int mxfp4_moe_align(const void* topk_ids, int ids_dtype, int64_t num_routes,
+                               int num_experts, int block_m, int32_t* sorted_ids,
+                               int32_t* expert_ids, int32_t* num_post_padded, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  int rc = check_align_args(num_routes, num_experts, block_m, ids_dtype);
+  if (rc) return rc;
+  int64_t ms, mb, nchunks;
+  align_capacity(num_routes, num_experts, block_m, &ms, &mb, &nchunks);
+  if (workspace_bytes < (nchunks > 0 ? nchunks : 1) * num_experts * 4) {
+    set_error("routing workspace too small");
+    return MXFP4_ERR_VALUE;
+  }
+  return do_align(topk_ids, ids_dtype, num_routes, num_experts, block_m, sorted_ids, expert_ids,
+                  num_post_padded, static_cast<int32_t*>(workspace), nchunks,
+                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
+                              const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,
+                              int64_t num_experts, int64_t n, int64_t k, void* c, int c_dtype,
+                              int64_t c_row_stride, const float* a_scale, const float* b_scale,
+                              const float* topk_weights, int mul_routed_weight,
+                              const int32_t* sorted_ids, const int32_t* expert_ids,
+                              const int32_t* num_post_padded, int64_t em, int block_m,
+                              int64_t num_valid, int top_k, void* stream) {
+  if (c_dtype != MXFP4_DT_BF16 && c_dtype != MXFP4_DT_F16 && c_dtype != MXFP4_DT_F32) {
+    set_error("unsupported software fallback compute dtype: %d", c_dtype);
+    return MXFP4_ERR_TYPE;
+  }
+  if (a_dtype == MXFP4_DT_U8 && a_mx == nullptr) {
+    set_error("packed MXFP4 activations require A_mx_scale");
+    return MXFP4_ERR_VALUE;
+  }
+  if (k <= 0 || k % 32 != 0 || n <= 0 || n > 0x7FFFFFFF || k > 0x7FFFFFFF || num_experts < 1 ||
+      top_k < 1 || block_m < 16 || block_m % 16 != 0 || em < 0 || em % block_m != 0) {
+    set_error("moe gemm: invalid sizes (n %lld, k %lld, block_m %d, em %lld)", (long long)n,
+              (long long)k, block_m, (long long)em);
+    return MXFP4_ERR_VALUE;
+  }
+  if (!aligned16(a) || !aligned16(b) || (a_dtype != MXFP4_DT_U8 && (a_row_stride * elem_size(a_dtype)) % 16) ||
+      (a_dtype == MXFP4_DT_U8 && a_row_stride % 16)) {
+    set_error("moe gemm: activation/weight rows must be 16-byte aligned");
+    return MXFP4_ERR_VALUE;
+  }
+  if (em == 0) return MXFP4_OK;
+  GemmArgs g = {};
+  g.a = a;
+  g.a_mx = a_mx;
+  g.lda = a_row_stride;
+  g.lda_mx = k / 32;
+  g.b = b;
+  g.bs = b_mx;
+  g.b_n = k / 2;
+  g.b_e = n * (k / 2);
+  g.bs_n = k / 32;
+  g.bs_e = n * (k / 32);
+  g.c = c;
+  g.ldc = c_row_stride;
+  g.sorted_ids = sorted_ids;
+  g.expert_ids = expert_ids;
+  g.num_post_padded = num_post_padded;
+  g.a_scale = a_scale;
+  g.b_scale = b_scale;
+  g.route_w = mul_routed_weight ? topk_weights : nullptr;
+  g.m = em;
+  g.num_valid = num_valid;
+  g.n = (int32_t)n;
+  g.k = (int32_t)k;
+  g.top_k = top_k;
+  g.block_m = block_m;
+  (void)a_rows;
+  return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mxfp4_linear_w4a16(const void* x, int x_dtype, int64_t m, int64_t k,
+                                  int64_t x_row_stride, const uint8_t* packed,
+                                  const uint8_t* scales, int64_t n, const void* bias, void* out,
+                                  void* stream) {
+  if (x_dtype != MXFP4_DT_BF16 && x_dtype != MXFP4_DT_F16) {
+    set_error("x must be fp16 or bf16, got dtype %d", x_dtype);
+    return MXFP4_ERR_TYPE;
+  }
+  if (k <= 0 || k % 128 != 0) {
+    set_error("logical K must be divisible by 128, got %lld", (long long)k);
+    return MXFP4_ERR_VALUE;
+  }
+  if (n <= 0 || n > 0x7FFFFFFF || k > 0x7FFFFFFF || m < 0) {
+    set_error("linear: invalid sizes");
+    return MXFP4_ERR_VALUE;
+  }
+  if (!aligned16(x) || !aligned16(packed) || (x_row_stride * 2) % 16 || x_row_stride < k) {
+    set_error("linear: activation/weight rows must be 16-byte aligned");
+    return MXFP4_ERR_VALUE;
+  }
+  if (m == 0) return MXFP4_OK;
+  GemmArgs g = {};
+  g.a = x;
+  g.lda = x_row_stride;
+  g.b = packed;
+  g.bs = scales;
+  g.b_n = k / 2;
+  g.bs_n = k / 32;
+  g.c = out;
+  g.ldc = n;
+  g.bias = bias;
+  g.m = m;
+  g.num_valid = m;
+  g.n = (int32_t)n;
+  g.k = (int32_t)k;
+  g.top_k = 1;
+  g.block_m = 16;
+  return launch_w4a16(g, x_dtype, EPI_STORE, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mxfp4_linear_w4a4(const uint8_t* a, const uint8_t* a_mx, int64_t m, int64_t k,
+                                 const uint8_t* b, const uint8_t* b_mx, int64_t n, void* out,
+                                 int out_dtype, void* stream) {
+  if (out_dtype != MXFP4_DT_BF16 && out_dtype != MXFP4_DT_F16 && out_dtype != MXFP4_DT_F32) {
+    set_error("w4a4: unsupported output dtype %d", out_dtype);
+    return MXFP4_ERR_TYPE;
+  }
+  if (k <= 0 || k % 32 != 0 || n <= 0 || m < 0 || n > 0x7FFFFFFF || k > 0x7FFFFFFF) {
+    set_error("logical K must be divisible by 32, got %lld", (long long)k);
+    return MXFP4_ERR_VALUE;
+  }
+  if (!aligned16(a) || !aligned16(b)) {
+    set_error("w4a4: packed rows must be 16-byte aligned");
+    return MXFP4_ERR_VALUE;
+  }
+  if (m == 0) return MXFP4_OK;
+  GemmArgs g = {};
+  g.a = a;
+  g.a_mx = a_mx;
+  g.lda = k / 2;
+  g.lda_mx = k / 32;
+  g.b = b;
+  g.bs = b_mx;
+  g.b_n = k / 2;
+  g.bs_n = k / 32;
+  g.c = out;
+  g.ldc = n;
+  g.m = m;
+  g.num_valid = m;
+  g.n = (int32_t)n;
+  g.k = (int32_t)k;
+  g.top_k = 1;
+  g.block_m = 16;
+  return launch_w4a4(g, out_dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mxfp4_moe_layer_workspace_size(int64_t m, int top_k, int num_experts,
+                                              int64_t hidden, int64_t inter, int64_t* bytes) {
+  if (m < 0 || top_k < 1 || num_experts < 1 || num_experts > kMaxExperts || hidden <= 0 ||
+      inter <= 0) {
+    set_error("moe layer: invalid sizes");
+    return MXFP4_ERR_VALUE;
+  }
+  *bytes = plan_layer(m, top_k, num_experts, hidden, inter, 2).total;
+  return MXFP4_OK;
+}
+
+extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hidden,
+                               const uint8_t* w13, const uint8_t* s13, const uint8_t* w2,
+                               const uint8_t* s2, int num_experts, int64_t inter,
+                               const float* topk_weights, const void* topk_ids, int ids_dtype,
+                               int top_k, void* out, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+  if (x_dtype != MXFP4_DT_BF16 && x_dtype != MXFP4_DT_F16) {
+    set_error("moe layer: x must be fp16 or bf16");
+    return MXFP4_ERR_TYPE;
+  }
+  if (hidden % 32 || inter % 32 || hidden <= 0 || inter <= 0 || hidden > 0x3FFFFFFF ||
+      inter > 0x3FFFFFFF) {
+    set_error("moe layer: hidden and intermediate sizes must be multiples of 32");
+    return MXFP4_ERR_VALUE;
+  }
+  int rc = check_align_args(m * top_k, num_experts, 16, ids_dtype);
+  if (rc) return rc;
+  if (!aligned16(x) || !aligned16(w13) || !aligned16(w2) || !aligned16(out) ||
+      !aligned16(workspace)) {
+    set_error("moe layer: buffers must be 16-byte aligned");
+    return MXFP4_ERR_VALUE;
+  }
+  const LayerPlan p = plan_layer(m, top_k, num_experts, hidden, inter, 2);
+  if (workspace_bytes < p.total) {
+    set_error("moe layer: workspace too small (%lld < %lld)", (long long)workspace_bytes,
+              (long long)p.total);
+    return MXFP4_ERR_VALUE;
+  }
+  if (m == 0) return MXFP4_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + p.off_counts);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws + p.off_sorted);
+  int32_t* experts = reinterpret_cast<int32_t*>(ws + p.off_experts);
+  int32_t* npp = reinterpret_cast<int32_t*>(ws + p.off_npp);
+  void* h = ws + p.off_h;
+  void* d = ws + p.off_d;
+
+  rc = do_align(topk_ids, ids_dtype, p.routes, num_experts, p.block_m, sorted, experts, npp,
+                counts, p.nchunks, st);
+  if (rc) return rc;
+
+  // gate_up with the fused SiLU*mul epilogue: h[r, :inter]
+  GemmArgs g = {};
+  g.a = x;
+  g.lda = hidden;
+  g.b = w13;
+  g.bs = s13;
+  g.b_n = hidden / 2;
+  g.b_e = 2 * inter * (hidden / 2);
+  g.bs_n = hidden / 32;
+  g.bs_e = 2 * inter * (hidden / 32);
+  g.c = h;
+  g.ldc = inter;
+  g.sorted_ids = sorted;
+  g.expert_ids = experts;
+  g.num_post_padded = npp;
+  g.m = p.max_sorted;
+  g.num_valid = p.routes;
+  g.n = (int32_t)inter;
+  g.k = (int32_t)hidden;
+  g.top_k = top_k;
+  g.block_m = p.block_m;
+  g.inter = (int32_t)inter;
+  rc = launch_w4a16(g, x_dtype, EPI_SILU_MUL, st);
+  if (rc) return rc;
+
+  // down with the route weight: d[r, :hidden]
+  GemmArgs g2 = g;
+  g2.a = h;
+  g2.lda = inter;
+  g2.b = w2;
+  g2.bs = s2;
+  g2.b_n = inter / 2;
+  g2.b_e = hidden * (inter / 2);
+  g2.bs_n = inter / 32;
+  g2.bs_e = hidden * (inter / 32);
+  g2.c = d;
+  g2.ldc = hidden;
+  g2.route_w = topk_weights;
+  g2.n = (int32_t)hidden;
+  g2.k = (int32_t)inter;
+  g2.top_k = 1;
+  g2.inter = 0;
+  rc = launch_w4a16(g2, x_dtype, EPI_STORE, st);
+  if (rc) return rc;
+
+  // top-k combine
+  const int64_t total = m * (hidden / 8);
+  const int grid = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+  if (x_dtype == MXFP4_DT_BF16) {
+    if (ids_dtype == MXFP4_DT_I32)
+      topk_sum<__bf16, int32_t><<<grid, 256, 0, st>>>(static_cast<const __bf16*>(d),
+                                                      static_cast<const int32_t*>(topk_ids), m,
+                                                      top_k, hidden, num_experts,
+                                                      static_cast<__bf16*>(out));
+    else
+      topk_sum<__bf16, int64_t><<<grid, 256, 0, st>>>(static_cast<const __bf16*>(d),
+                                                      static_cast<const int64_t*>(topk_ids), m,
+                                                      top_k, hidden, num_experts,
+                                                      static_cast<__bf16*>(out));
+  } else {
+    if (ids_dtype == MXFP4_DT_I32)
+      topk_sum<_Float16, int32_t><<<grid, 256, 0, st>>>(static_cast<const _Float16*>(d),
+                                                        static_cast<const int32_t*>(topk_ids), m,
+                                                        top_k, hidden, num_experts,
+                                                        static_cast<_Float16*>(out));
+    else
+      topk_sum<_Float16, int64_t><<<grid, 256, 0, st>>>(static_cast<const _Float16*>(d),
+                                                        static_cast<const int64_t*>(topk_ids), m,
+                                                        top_k, hidden, num_experts,
+                                                        static_cast<_Float16*>(out));
+  }
+  return launch_status("moe topk sum launch");
+}

@@ -1,0 +1,301 @@
+# SPDX-License-Identifier: MIT
+"""MI355X (gfx950) implementation of the ``moe_op_mxfp4_soft`` operator surface.
+
+Same names, signatures, argument meaning and exception behaviour as the
+reference module ``src/aiter/ops/triton/moe_op_mxfp4_soft.py`` of
+lutianshu824/mxfp4-gfx936 ("soft" below), so callers and tests written for
+it run unchanged; every function computes through hand-written HIP kernels in
+``libmxfp4_gfx950.so`` on the tensor's device and stream.  There is one
+backend: the reference's env switch ``MXFP4_GFX936_BACKEND`` is still
+validated (soft:45-49) but both of its values run the HIP kernels.
+
+This file can be imported as ``mxfp4_amd.moe_op_mxfp4_soft`` or loaded by
+path with importlib, as the reference tests load their module (test:10-19).
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import torch
+
+try:
+    from . import _lib
+except ImportError:  # loaded by file path, outside its package
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    from mxfp4_amd import _lib  # type: ignore[no-redef]
+
+# soft:12-29 (OCP E2M1 code -> value; bit 3 is the sign)
+_MXFP4_E2M1_VALUES = (
+    0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+    -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0,
+)
+
+_KERNEL_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _backend() -> str:
+    """soft:45-49: ``MXFP4_GFX936_BACKEND`` in {safe, triton}, default safe;
+    anything else fails loudly.  Both values select the HIP kernels here."""
+    backend = os.getenv("MXFP4_GFX936_BACKEND", "safe")
+    if backend not in ("safe", "triton"):
+        raise ValueError(f"unknown gfx936 MXFP4 backend: {backend}")
+    return backend
+
+
+def _routing_block_m(num_routes: int, num_experts: int) -> int:
+    """Rows per expert block for the routed GEMMs, from the mean rows per expert."""
+    avg = num_routes / max(num_experts, 1)
+    if avg <= 8:
+        return 16
+    if avg <= 20:
+        return 32
+    if avg <= 80:
+        return 64
+    return 128
+
+
+def dequant_mxfp4(
+    packed: torch.Tensor,
+    block_scales: torch.Tensor,
+    dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """Dequantize packed OCP MXFP4 E2M1 values with E8M0 block scales.
+
+    soft:277-307.  out[..., k] = E2M1[nibble(k)] * 2**(s[..., k//32] - 127),
+    evaluated exactly in FP32 and rounded once to ``dtype`` (RNE), with the
+    low nibble as the even k; s = 255 gives NaN.  Bit-exact with the
+    reference for float32 / bfloat16 / float16 outputs; other float dtypes
+    are converted from the exact FP32 result, as the reference's ``.to``.
+    """
+    if packed.dtype != torch.uint8:
+        raise TypeError(f"packed must be uint8, got {packed.dtype}")
+    if block_scales.dtype != torch.uint8:
+        raise TypeError(f"block_scales must be uint8, got {block_scales.dtype}")
+
+    logical_k = packed.shape[-1] * 2
+    if logical_k % 32 != 0:
+        raise ValueError(f"logical K must be divisible by 32, got {logical_k}")
+    if block_scales.shape[:-1] != packed.shape[:-1]:
+        raise ValueError("packed and block_scales leading dimensions must match")
+    if block_scales.shape[-1] * 32 != logical_k:
+        raise ValueError("one E8M0 scale is required for every 32 MXFP4 values")
+
+    device = _lib.require_device(packed, block_scales)
+    lib = _lib.load()
+    kernel_dtype = dtype if dtype in _KERNEL_DTYPES else torch.float32
+    out_shape = (*packed.shape[:-1], logical_k)
+    out = torch.empty(out_shape, dtype=kernel_dtype, device=device)
+    rows = out.numel() // logical_k if logical_k else 0
+    if rows and logical_k:
+        p = _lib.aligned(packed.reshape(rows, logical_k // 2))
+        s = block_scales.reshape(rows, logical_k // 32).contiguous()
+        with torch.cuda.device(device):
+            _lib.check(lib.mxfp4_dequant(
+                _lib.ptr(p), p.stride(0), _lib.ptr(s), s.stride(0), rows, logical_k,
+                _lib.ptr(out), _lib.dtype_code(kernel_dtype), _lib.stream_of(device)))
+    return out if kernel_dtype == dtype else out.to(dtype)
+
+
+def linear_mxfp4_soft(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    block_scales: torch.Tensor,
+    bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Weight-only OCP MXFP4 linear: ``x @ dequant(packed, block_scales).T (+ bias)``.
+
+    soft:310-376.  BF16/FP16 activations, FP32 accumulation, one rounding to
+    x.dtype.  A bias of x's dtype and shape [N] is fused into the epilogue;
+    any other bias is added afterwards with torch's promotion, as the
+    reference does (soft:374-375).
+    """
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError(f"x must be fp16 or bf16, got {x.dtype}")
+    if packed.dtype != torch.uint8 or block_scales.dtype != torch.uint8:
+        raise TypeError("packed weights and E8M0 scales must be uint8")
+    if packed.ndim != 2 or block_scales.ndim != 2:
+        raise ValueError("linear weights and scales must be 2D")
+    logical_k = packed.shape[1] * 2
+    if x.shape[-1] != logical_k:
+        raise ValueError(f"input K {x.shape[-1]} does not match weight K {logical_k}")
+    if logical_k % 128 != 0:
+        raise ValueError(f"logical K must be divisible by 128, got {logical_k}")
+    if block_scales.shape != (packed.shape[0], logical_k // 32):
+        raise ValueError("one E8M0 scale is required for every 32 MXFP4 values")
+
+    input_shape = x.shape
+    _backend()
+    device = _lib.require_device(x, packed, block_scales, bias)
+    lib = _lib.load()
+    n = packed.shape[0]
+    x_2d = _lib.aligned(x.reshape(-1, logical_k))
+    w = _lib.aligned(packed)
+    s = block_scales.contiguous()
+    fuse_bias = (bias is not None and bias.dtype == x.dtype and bias.ndim == 1
+                 and bias.shape[0] == n)
+    b = bias.contiguous() if fuse_bias else None
+    output = torch.empty((x_2d.shape[0], n), dtype=x.dtype, device=device)
+    if x_2d.shape[0] and n:
+        with torch.cuda.device(device):
+            _lib.check(lib.mxfp4_linear_w4a16(
+                _lib.ptr(x_2d), _lib.dtype_code(x.dtype), x_2d.shape[0], logical_k,
+                x_2d.stride(0), _lib.ptr(w), _lib.ptr(s), n, _lib.ptr(b), _lib.ptr(output),
+                _lib.stream_of(device)))
+    if bias is not None and not fuse_bias:
+        output = output + bias
+    return output.reshape(*input_shape[:-1], n)
+
+
+def make_routing_device(topk_ids: torch.Tensor, num_experts: int, block_m: int):
+    """Device-side routing metadata (the vllm:119-146 format) without a host
+    sync.  Returns (sorted_ids, expert_ids, num_tokens_post_padded), the first
+    two sized to their capacity; entries at or beyond
+    ``num_tokens_post_padded[0]`` (resp. its block count) are unused."""
+    device = _lib.require_device(topk_ids)
+    lib = _lib.load()
+    ids = topk_ids.reshape(-1)
+    if ids.dtype not in (torch.int32, torch.int64):
+        ids = ids.to(torch.int64)
+    ids = ids.contiguous()
+    n = ids.numel()
+    import ctypes
+    ms, mb, wsb = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(lib.mxfp4_moe_align_sizes(n, num_experts, block_m, ctypes.byref(ms),
+                                         ctypes.byref(mb), ctypes.byref(wsb)))
+    sorted_ids = torch.empty(ms.value, dtype=torch.int32, device=device)
+    expert_ids = torch.empty(mb.value, dtype=torch.int32, device=device)
+    npp = torch.empty(1, dtype=torch.int32, device=device)
+    ws = torch.empty(max(wsb.value // 4, 1), dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        _lib.check(lib.mxfp4_moe_align(
+            _lib.ptr(ids), _lib.dtype_code(ids.dtype), n, num_experts, block_m,
+            _lib.ptr(sorted_ids), _lib.ptr(expert_ids), _lib.ptr(npp), _lib.ptr(ws),
+            wsb.value, _lib.stream_of(device)))
+    return sorted_ids, expert_ids, npp
+
+
+def _moe_gemm_launch(A, A_mx_scale, B, B_mx_scale, C2d, A_scale, B_scale, topk_weights,
+                     mul_routed_weight, sorted_ids, expert_ids, npp, block_m, num_valid,
+                     top_k, device):
+    """Launch the routed grouped GEMM writing rows of the contiguous 2-D view
+    ``C2d`` [routes, N]."""
+    lib = _lib.load()
+    num_experts, n, k = B.shape[0], B.shape[1], B.shape[2] * 2
+    a_code = _lib.dtype_code(A.dtype)
+    a_row_stride = A.stride(0)
+    with torch.cuda.device(device):
+        _lib.check(lib.mxfp4_moe_gemm(
+            _lib.ptr(A), a_code, A.shape[0], a_row_stride, _lib.ptr(A_mx_scale), _lib.ptr(B),
+            _lib.ptr(B_mx_scale), num_experts, n, k, _lib.ptr(C2d), _lib.dtype_code(C2d.dtype),
+            C2d.stride(0), _lib.ptr(A_scale), _lib.ptr(B_scale), _lib.ptr(topk_weights),
+            1 if mul_routed_weight else 0, _lib.ptr(sorted_ids), _lib.ptr(expert_ids),
+            _lib.ptr(npp), sorted_ids.numel(), block_m, num_valid, top_k,
+            _lib.stream_of(device)))
+
+
+def _prepare_moe_operands(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights,
+                          topk_ids, top_k):
+    """Shared shape checks and layout normalisation for the routed GEMM."""
+    matmul_dtype = C.dtype
+    if B.ndim != 3 or B_mx_scale.shape != (B.shape[0], B.shape[1], B.shape[2] * 2 // 32):
+        raise ValueError("B must be [E, N, K/2] with B_mx_scale [E, N, K/32]")
+    logical_k = B.shape[2] * 2
+    if logical_k % 32 != 0:
+        raise ValueError(f"logical K must be divisible by 32, got {logical_k}")
+    if A.dtype == torch.uint8:
+        if A_mx_scale is None:
+            raise ValueError("packed MXFP4 activations require A_mx_scale")
+        if A.ndim != 2 or A.shape[1] * 2 != logical_k or A_mx_scale.shape != (
+                A.shape[0], logical_k // 32):
+            raise RuntimeError("packed activations must be [M, K/2] with A_mx_scale [M, K/32]")
+        if A_mx_scale.dtype != torch.uint8:
+            raise TypeError("A_mx_scale must be uint8")
+        act = _lib.aligned(A)
+        act_mx = A_mx_scale.contiguous()
+    else:
+        if A_mx_scale is not None:
+            raise ValueError("unpacked activations must not provide A_mx_scale")
+        if A.ndim != 2 or A.shape[1] != logical_k:
+            raise RuntimeError(f"activations must be [M, {logical_k}], got {tuple(A.shape)}")
+        act = A if A.dtype == matmul_dtype else A.to(matmul_dtype)
+        act = _lib.aligned(act)
+        act_mx = None
+    m = topk_ids.shape[0]
+    if C.shape != (m, top_k, B.shape[1]):
+        raise RuntimeError(
+            f"C must be [M, top_k, N] = {(m, top_k, B.shape[1])}, got {tuple(C.shape)}")
+    if act.shape[0] < m:
+        raise RuntimeError("fewer activation rows than top-k rows")
+    a_scale = A_scale.reshape(-1)[:1].to(torch.float32).contiguous()
+    if B_scale.numel() < B.shape[0]:
+        raise RuntimeError("B_scale must hold one scale per expert")
+    b_scale = B_scale.reshape(-1).to(torch.float32).contiguous()
+    weights = topk_weights.to(torch.float32).contiguous()
+    ids = topk_ids if topk_ids.dtype in (torch.int32, torch.int64) else topk_ids.to(torch.int64)
+    ids = ids.contiguous()
+    return act, act_mx, _lib.aligned(B), B_mx_scale.contiguous(), a_scale, b_scale, weights, ids
+
+
+def fused_moe_mxfp4_soft(
+    A: torch.Tensor,
+    B: torch.Tensor,
+    C: torch.Tensor,
+    A_scale: torch.Tensor,
+    B_scale: torch.Tensor,
+    A_mx_scale: torch.Tensor | None,
+    B_mx_scale: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    mul_routed_weight: bool,
+    top_k: int,
+    swizzle_mx_a: bool,
+    swizzle_mx_b: bool,
+) -> None:
+    """Routed MXFP4 MoE GEMM writing ``C`` [M, top_k, N] in place.
+
+    soft:379-494 (safe semantics): C is zero-filled, then for every (token t,
+    slot s) whose expert e = topk_ids[t, s] is in [0, E):
+    C[t, s] = A[t] . dequant(B[e])^T * A_scale[0] * B_scale[e]
+    (* topk_weights[t, s] when ``mul_routed_weight``), FP32 accumulation, one
+    rounding to C.dtype.  A is bf16/fp16/fp32 (converted to C.dtype, soft:475)
+    or packed MXFP4 with ``A_mx_scale`` (W4A4 on the block-scaled MFMA).
+    Like the reference's safe path, the routing metadata arguments are not
+    consulted (soft:466): routing is rebuilt on the device from ``topk_ids``
+    with no host synchronisation.
+    """
+    if swizzle_mx_a or swizzle_mx_b:
+        raise NotImplementedError("the gfx936 software fallback does not support swizzled scales")
+    if topk_ids.shape != topk_weights.shape or topk_ids.shape[1] != top_k:
+        raise ValueError("top-k ids and weights must have matching (M, top_k) shapes")
+    if B.dtype != torch.uint8 or B_mx_scale is None:
+        raise TypeError("the gfx936 software fallback requires packed MXFP4 weights")
+
+    matmul_dtype = C.dtype
+    if matmul_dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"unsupported software fallback compute dtype: {matmul_dtype}")
+
+    _backend()
+    del sorted_token_ids, expert_ids, num_tokens_post_padded
+    device = _lib.require_device(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale,
+                                 topk_weights, topk_ids)
+    act, act_mx, b, b_mx, a_scale, b_scale, weights, ids = _prepare_moe_operands(
+        A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights, topk_ids, top_k)
+
+    C.zero_()
+    num_routes = ids.numel()
+    if num_routes == 0 or C.numel() == 0:
+        return
+    block_m = _routing_block_m(num_routes, B.shape[0])
+    sorted_ids, expert_blk, npp = make_routing_device(ids, B.shape[0], block_m)
+    out = C if C.is_contiguous() and C.data_ptr() % 16 == 0 else torch.zeros(
+        C.shape, dtype=C.dtype, device=device)
+    _moe_gemm_launch(act, act_mx, b, b_mx, out.view(num_routes, B.shape[1]), a_scale, b_scale,
+                     weights, mul_routed_weight, sorted_ids, expert_blk, npp, block_m, num_routes,
+                     top_k, device)
+    if out is not C:
+        C.copy_(out)

@@ -1,0 +1,170 @@
+"""GPU parity: standalone dequant (bit-exact) and the dense W4A16 linear
+(tolerance vs the FP64 oracle, and no worse than the reference safe path
+``x @ dequant(W).T`` run through torch on the same device)."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import mxfp4_amd as mx
+from mxfp4_amd import _lib
+from oracle import c_oracle, mxfp4_oracle as O
+
+from _helpers import assert_parity, cuda, rand_act, rand_mxfp4
+
+pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::RuntimeWarning")]
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+IDT = {"f32": torch.int32, "bf16": torch.int16, "f16": torch.int16}
+
+
+def _bits(t: torch.Tensor, dt: str) -> np.ndarray:
+    a = t.view(IDT[dt]).cpu().numpy()
+    return a.view(np.uint32 if dt == "f32" else np.uint16)
+
+
+def test_native_library_is_loaded():
+    lib = _lib.load()
+    assert lib.mxfp4_abi_version() == _lib.ABI_VERSION
+    assert torch.cuda.is_available()
+
+
+# ---------------------------------------------------------------- dequant
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_dequant_all_codes_all_scales_bitexact(dt):
+    g = np.load(os.path.join(GOLDEN, "dequant_table.npz"))
+    out = mx.dequant_mxfp4(cuda(g["packed"]), cuda(g["scales"]), TDT[dt])
+    # every pattern, including the canonical NaN of s = 255, -0, subnormals, +-inf
+    assert np.array_equal(_bits(out, dt), g[dt])
+
+
+def test_dequant_reference_known_answer():
+    # tests/test_moe_mxfp4_soft.py:81-92
+    packed = torch.tensor([[c | ((c + 1) << 4) for c in range(0, 16, 2)] * 2], dtype=torch.uint8,
+                          device="cuda")
+    scales = torch.full((1, 1), 127, device="cuda", dtype=torch.uint8)
+    actual = mx.dequant_mxfp4(packed, scales)
+    expected = torch.tensor([mx._MXFP4_E2M1_VALUES], device="cuda", dtype=torch.float32).repeat(1, 2)
+    torch.testing.assert_close(actual, expected, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_dequant_expert_shapes_vs_c_oracle(dt):
+    rng = np.random.default_rng(20260901)
+    # leading dims [E, N] like the MoE expert tensors; the full scale range
+    packed, scales = rand_mxfp4(rng, (3, 96), 2048, lo=0, hi=255)
+    out = mx.dequant_mxfp4(cuda(packed), cuda(scales), TDT[dt])
+    assert out.shape == (3, 96, 2048)
+    assert np.array_equal(_bits(out, dt), c_oracle.dequant_bits(packed, scales, dt))
+
+
+def test_dequant_noncontiguous_and_other_dtype():
+    rng = np.random.default_rng(7)
+    packed, scales = rand_mxfp4(rng, (64,), 256)
+    p = cuda(packed)[::2]
+    s = cuda(scales)[::2]
+    out = mx.dequant_mxfp4(p, s, torch.bfloat16)
+    assert np.array_equal(_bits(out, "bf16"), O.dequant_bits(packed[::2], scales[::2], "bf16"))
+    out64 = mx.dequant_mxfp4(p, s, torch.float64)
+    assert out64.dtype == torch.float64
+    assert np.array_equal(out64.cpu().numpy(), O.dequant_f32(packed[::2], scales[::2]).astype(np.float64))
+    empty = mx.dequant_mxfp4(torch.empty((0, 16), dtype=torch.uint8, device="cuda"),
+                             torch.empty((0, 1), dtype=torch.uint8, device="cuda"))
+    assert empty.shape == (0, 32)
+
+
+# ---------------------------------------------------------------- linear
+
+def _safe_reference(x: torch.Tensor, packed: np.ndarray, scales: np.ndarray) -> torch.Tensor:
+    """soft:371-373 on the device: exact dequant (oracle bits) then torch.matmul."""
+    dt = "bf16" if x.dtype == torch.bfloat16 else "f16"
+    w = torch.from_numpy(O.dequant_bits(packed, scales, dt).view(np.int16)).view(x.dtype).cuda()
+    return torch.matmul(x.reshape(-1, w.shape[1]), w.T)
+
+
+@pytest.mark.parametrize("m_value", [1, 8])
+def test_linear_matches_explicit_dequant_small(m_value):
+    # test:95-111 with the reference's quantizer on randn weights
+    torch.manual_seed(20260811 + m_value)
+    n_value, k_value = 64, 128
+    x = torch.randn((m_value, k_value), dtype=torch.bfloat16)
+    w = torch.randn((n_value, k_value), dtype=torch.bfloat16)
+    packed, scales = O.quant_mxfp4_ties_away(w.float().numpy())
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    assert y.dtype == torch.bfloat16 and y.shape == (m_value, n_value)
+    ref = _safe_reference(cuda(x), packed, scales)
+    assert_parity(y, O.linear_fp64(x.float().numpy(), packed, scales), ref=ref)
+
+
+@pytest.mark.parametrize("k,n", [(2048, 5120), (4096, 2048)], ids=["qkv", "o_proj"])
+@pytest.mark.parametrize("m", [1, 8, 370, 4096])
+def test_linear_attention_shapes(m, k, n):
+    rng = np.random.default_rng(20260810 + m + k)
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    x = rand_act(20260810 + m, (m, k))
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    ref = _safe_reference(cuda(x), packed, scales)
+    rows = np.arange(m) if m <= 370 else np.sort(rng.choice(m, 192, replace=False))
+    oracle = O.linear_fp64(x.float().numpy()[rows], packed, scales)
+    assert_parity(y[rows], oracle, ref=ref[rows], what=f"linear m={m} k={k} n={n}")
+
+
+@pytest.mark.parametrize("m", [1, 20, 100])
+def test_linear_fp16_partial_tiles(m):
+    rng = np.random.default_rng(m)
+    n, k = 200, 768
+    packed, scales = rand_mxfp4(rng, (n,), k, lo=118, hi=132)
+    x = rand_act(m, (m, k), torch.float16)
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    assert y.dtype == torch.float16
+    ref = _safe_reference(cuda(x), packed, scales)
+    oracle = O.linear_fp64(x.float().numpy(), packed, scales, w_dtype="f16")
+    assert_parity(y, oracle, ref=ref, what=f"fp16 m={m}")
+
+
+def test_linear_bias_and_leading_dims():
+    rng = np.random.default_rng(31)
+    n, k = 96, 256
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    x = rand_act(31, (2, 3, k))
+    bias = rand_act(32, (n,))
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales), cuda(bias))
+    assert y.shape == (2, 3, n) and y.dtype == torch.bfloat16
+    oracle = O.linear_fp64(x.float().numpy().reshape(6, k), packed, scales, bias.float().numpy())
+    assert_parity(y.reshape(6, n), oracle)
+    # an fp32 bias is added after the GEMM with torch's promotion (soft:374-375):
+    # exactly the bf16 GEMM result plus the bias in fp32
+    y32 = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales), cuda(bias.float()))
+    assert y32.dtype == torch.float32
+    y0 = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    assert torch.equal(y32, y0 + cuda(bias.float()))
+
+
+@pytest.mark.parametrize("scale", [1, 254])
+@pytest.mark.parametrize("m", [1, 40])
+def test_linear_edge_sweep_every_code(scale, m):
+    # BASELINE config 5 edge sweep: every E2M1 code at E8M0 1 and 254, K=768
+    n, k = 32, 768
+    codes = np.tile(np.arange(16, dtype=np.uint8), (n, k // 16))
+    for r in range(n):
+        codes[r] = np.roll(codes[r], r)
+    packed = O.pack_codes(codes)
+    scales = np.full((n, k // 32), scale, dtype=np.uint8)
+    x = rand_act(900 + m, (m, k))
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales)).float().cpu().numpy()
+    with np.errstate(all="ignore"):
+        oracle = O.linear_fp64(x.float().numpy(), packed, scales)
+    if scale == 254:
+        # +-inf weights: the IEEE outcome (NaN where +inf and -inf meet) is
+        # independent of summation order and must match exactly.
+        assert np.array_equal(np.isnan(y), np.isnan(oracle))
+        fin = ~np.isnan(oracle)
+        assert np.array_equal(y[fin], oracle[fin])  # all +-inf
+    else:
+        assert np.all(np.isfinite(y))
+        assert_parity(y, oracle, what="scale 1 (subnormal weights)")

@@ -1,0 +1,248 @@
+"""GPU parity: routed MoE (soft op, AITER entry, device routing, the vLLM MoE
+layer) against the FP64 oracle, the reference's per-(token, slot) GEMV loop
+(test:270-285) and the reference safe path."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mxfp4_amd as mx
+from oracle import c_oracle, mxfp4_oracle as O
+
+from _helpers import assert_layer_parity, assert_parity, cuda, rand_act, rand_mxfp4
+
+pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::RuntimeWarning")]
+
+
+def _route(m, num_experts, top_k, seed):
+    """softmax -> top-k -> renormalize of seeded router logits."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn((m, num_experts), generator=g)
+    p = torch.softmax(logits, dim=-1)
+    w, ids = torch.topk(p, k=top_k, dim=-1)
+    return (w / w.sum(-1, keepdim=True)).float(), ids
+
+
+def _empty():
+    return torch.empty(0, device="cuda")
+
+
+# ---------------------------------------------------------------- soft op
+
+@pytest.mark.parametrize("m_value", [1, 2, 4, 8, 64])
+@pytest.mark.parametrize("quantize_activations", [False, True])
+@pytest.mark.parametrize("mul_routed_weight", [False, True])
+def test_fused_moe_matrix(m_value, quantize_activations, mul_routed_weight):
+    # test:216-285 (the 20-case operator matrix) on the HIP backend
+    torch.manual_seed(20260810 + m_value)
+    n_value, k_value, experts, top_k = 64, 128, 4, 2
+    activations = torch.randn((m_value, k_value), dtype=torch.bfloat16)
+    weights = torch.randn((experts, n_value, k_value), dtype=torch.bfloat16)
+    wp, ws = O.quant_mxfp4_ties_away(weights.float().numpy())
+    if quantize_activations:
+        ap, asc = O.quant_mxfp4_ties_away(activations.float().numpy())
+        kernel_a, kernel_amx = cuda(ap), cuda(asc)
+        ref_a = O.dequant_values(ap, asc, "bf16")
+    else:
+        kernel_a, kernel_amx = cuda(activations), None
+        ref_a = activations.float().numpy().astype(np.float64)
+    logits = torch.randn((m_value, experts), dtype=torch.float32)
+    topk_weights, topk_ids = torch.topk(torch.softmax(logits, dim=-1), k=top_k, dim=-1)
+    actual = torch.empty((m_value, top_k, n_value), device="cuda", dtype=torch.bfloat16)
+    scalar_a = torch.tensor([0.75], device="cuda")
+    scalar_b = torch.linspace(0.5, 1.25, experts, device="cuda")
+    mx.fused_moe_mxfp4_soft(kernel_a, cuda(wp), actual, scalar_a, scalar_b, kernel_amx, cuda(ws),
+                            cuda(topk_weights), cuda(topk_ids), _empty(), _empty(), _empty(),
+                            mul_routed_weight, top_k, False, False)
+    # the reference's own GEMV loop (test:270-281), on the device
+    dq = torch.from_numpy(O.dequant_bits(wp, ws, "bf16").view(np.int16)).view(torch.bfloat16).cuda()
+    ra = torch.from_numpy(ref_a.astype(np.float32)).to(torch.bfloat16).cuda()
+    expected = torch.empty_like(actual)
+    for t in range(m_value):
+        for s in range(top_k):
+            e = int(topk_ids[t, s])
+            v = torch.matmul(ra[t], dq[e].transpose(0, 1)) * scalar_a[0] * scalar_b[e]
+            if mul_routed_weight:
+                v = v * topk_weights[t, s].cuda()
+            expected[t, s] = v.to(expected.dtype)
+    # The loop rounds to bf16 after the matmul and after each scalar multiply
+    # (up to four roundings, test:274-281); the HIP epilogue applies the
+    # scales to the FP32 accumulator and rounds once, so the two may differ
+    # by two bf16 ulps (1.6% at the bottom of a binade).  The strict bar is
+    # the FP64 parity below, where ours must also be no worse than the loop.
+    torch.testing.assert_close(actual, expected, rtol=2e-2, atol=2e-2)
+    oracle = O.fused_moe_fp64(ref_a, wp, ws, 0.75, scalar_b.cpu().numpy(), topk_weights.numpy(),
+                              topk_ids.numpy(), mul_routed_weight)
+    assert_parity(actual, oracle, ref=expected)
+
+
+@pytest.mark.parametrize("c_dtype", [torch.float16, torch.float32])
+def test_fused_moe_compute_dtypes(c_dtype):
+    rng = np.random.default_rng(41)
+    m, k, n, e, top_k = 24, 256, 80, 6, 3
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(41, (m, k))  # bf16 activations converted to C.dtype (soft:475)
+    w, ids = _route(m, e, top_k, 42)
+    C = torch.empty((m, top_k, n), dtype=c_dtype, device="cuda")
+    mx.fused_moe_mxfp4_soft(cuda(a), cuda(wp), C, torch.ones(1, device="cuda"),
+                            torch.ones(e, device="cuda"), None, cuda(ws), cuda(w), cuda(ids),
+                            _empty(), _empty(), _empty(), True, top_k, False, False)
+    dt = "f16" if c_dtype == torch.float16 else "f32"
+    oracle = O.fused_moe_fp64(O.round_to_dtype(a.float().numpy(), dt), wp, ws, 1.0, np.ones(e),
+                              w.numpy(), ids.numpy(), True, compute_dtype=dt)
+    assert_parity(C, oracle, what=str(c_dtype))
+
+
+def test_fused_moe_out_of_range_ids_stay_zero():
+    rng = np.random.default_rng(43)
+    m, k, n, e, top_k = 5, 128, 48, 4, 2
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(43, (m, k))
+    ids = torch.tensor([[0, 1], [4, 2], [-1, 3], [1, 1], [9, 0]])
+    w = torch.rand((m, top_k))
+    C = torch.full((m, top_k, n), 5.0, dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4_soft(cuda(a), cuda(wp), C, torch.ones(1, device="cuda"),
+                            torch.ones(e, device="cuda"), None, cuda(ws), cuda(w), cuda(ids),
+                            _empty(), _empty(), _empty(), False, top_k, False, False)
+    out = C.float().cpu()
+    for t, s in ((1, 0), (2, 0), (4, 0)):
+        assert torch.all(out[t, s] == 0)
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 1.0, np.ones(e), w.numpy(),
+                              ids.numpy(), False)
+    assert_parity(C, oracle)
+
+
+@pytest.mark.parametrize("m", [1, 8, 32])
+def test_fused_moe_decode_shapes(m):
+    # BASELINE config 5 gate_up shape: E=128, top-8, K=2048 -> N=1536
+    rng = np.random.default_rng(20260820 + m)
+    e, k, n, top_k = 128, 2048, 1536, 8
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(20260820 + m, (m, k))
+    w, ids = _route(m, e, top_k, 20260830 + m)
+    C = torch.empty((m, top_k, n), dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4_soft(cuda(a), cuda(wp), C, torch.ones(1, device="cuda"),
+                            torch.ones(e, device="cuda"), None, cuda(ws), cuda(w), cuda(ids),
+                            _empty(), _empty(), _empty(), True, top_k, False, False)
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 1.0, np.ones(e), w.numpy(), ids.numpy(),
+                              True)
+    assert_parity(C, oracle, what=f"moe decode m={m}")
+
+
+# ---------------------------------------------------------------- AITER entry
+
+@pytest.mark.parametrize("block_m", [16, 32, 64, 128])
+def test_aiter_entry_uses_metadata(block_m):
+    rng = np.random.default_rng(block_m)
+    m, k, n, e, top_k = 40, 256, 96, 5, 2
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(block_m, (m, k))
+    w, ids = _route(m, e, top_k, 100 + block_m)
+    srt, exp_, npp = O.make_routing(ids.numpy(), block_m=block_m, num_experts=e)
+    # mark the blocks of expert 2 as not on this device (EP sentinel -1)
+    exp_ = exp_.copy()
+    exp_[exp_ == 2] = -1
+    C = torch.full((m, top_k, n), 3.0, dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4(cuda(a), cuda(wp), C, torch.tensor([0.5], device="cuda"),
+                       torch.linspace(1, 2, e, device="cuda"), None, cuda(ws), cuda(w), cuda(ids),
+                       cuda(srt), cuda(exp_), cuda(npp), True, top_k, False, False,
+                       {"BLOCK_SIZE_M": block_m}, torch.bfloat16)
+    out = C.float().cpu().numpy()
+    ids_np = ids.numpy()
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 0.5, np.linspace(1, 2, e), w.numpy(),
+                              ids_np, True)
+    oracle[ids_np == 2] = 0.0  # expert -1 blocks write zeros
+    assert_parity(out, oracle)
+
+
+# ---------------------------------------------------------------- routing
+
+@pytest.mark.parametrize("n_tokens,top_k,num_experts,block_m",
+                         [(1, 8, 128, 16), (8, 8, 128, 16), (33, 4, 16, 32), (512, 8, 128, 64),
+                          (700, 3, 7, 128), (4096, 8, 128, 128)])
+def test_device_routing_matches_oracle(n_tokens, top_k, num_experts, block_m):
+    g = torch.Generator().manual_seed(n_tokens * 7 + top_k)
+    ids = torch.randint(-1, num_experts + 1, (n_tokens, top_k), generator=g)
+    srt, exp_, npp = mx.make_routing(cuda(ids), block_m=block_m, num_experts=num_experts)
+    used = int(npp[0])
+    r_srt, r_exp, r_npp = c_oracle.make_routing(ids.numpy(), num_experts, block_m)
+    assert used == int(r_npp[0])
+    assert np.array_equal(srt[:used].cpu().numpy(), r_srt)
+    assert np.array_equal(exp_[:used // block_m].cpu().numpy(), r_exp)
+    # int32 ids give the same metadata
+    srt32, _, npp32 = mx.make_routing(cuda(ids.to(torch.int32)), block_m=block_m,
+                                      num_experts=num_experts)
+    assert int(npp32[0]) == used and torch.equal(srt32[:used], srt[:used])
+
+
+# ---------------------------------------------------------------- MoE layer
+
+def _layer_weights(seed, e=128, hidden=2048, inter=768):
+    rng = np.random.default_rng(seed)
+    w13, s13 = rand_mxfp4(rng, (e, 2 * inter), hidden)
+    w2, s2 = rand_mxfp4(rng, (e, hidden), inter)
+    return w13, s13, w2, s2
+
+
+@pytest.fixture(scope="module")
+def layer_weights():
+    return _layer_weights(20260815)
+
+
+@pytest.mark.parametrize("m", [1, 8, 32, 512, 4096])
+def test_moe_layer_vs_oracle(m, layer_weights):
+    w13, s13, w2, s2 = layer_weights
+    x = rand_act(20260816 + m, (m, 2048))
+    w, ids = _route(m, 128, 8, 20260817 + m)
+    y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
+    assert y.shape == (m, 2048) and y.dtype == torch.bfloat16
+    # each token depends only on its own row and routing: check a sample
+    rows = np.arange(m) if m <= 32 else np.sort(np.random.default_rng(m).choice(m, 32, False))
+    oracle = O.moe_layer_fp64(x.float().numpy()[rows], w13, s13, w2, s2, w.numpy()[rows],
+                              ids.numpy()[rows])
+    t = torch.from_numpy
+    safe = O.moe_layer_safe(x[rows], t(w13), t(s13), t(w2), t(s2), w[rows], ids[rows])
+    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what=f"moe layer m={m}")
+
+
+def test_moe_layer_small_vs_golden_and_safe():
+    import os
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "small_cases.npz"))
+    y = mx.moe_layer(cuda(torch.from_numpy(g["layer_x"]).to(torch.bfloat16)), cuda(g["layer_w13"]),
+                     cuda(g["layer_s13"]), cuda(g["layer_w2"]), cuda(g["layer_s2"]),
+                     cuda(g["layer_w"]), cuda(g["layer_ids"]))
+    t = lambda k: torch.from_numpy(g[k])  # noqa: E731
+    safe = O.moe_layer_safe(t("layer_x").to(torch.bfloat16), t("layer_w13"), t("layer_s13"),
+                            t("layer_w2"), t("layer_s2"), t("layer_w"), t("layer_ids"))
+    assert_layer_parity(y, g["layer_y"], safe)
+
+
+def test_moe_layer_fp16_and_invalid_ids():
+    rng = np.random.default_rng(5)
+    # small scales keep every fp16 intermediate finite
+    w13, s13 = rand_mxfp4(rng, (8, 256), 256, lo=116, hi=121)
+    w2, s2 = rand_mxfp4(rng, (8, 256), 128, lo=116, hi=121)
+    m = 12
+    x = rand_act(6, (m, 256), torch.float16)
+    w, ids = _route(m, 8, 2, 7)
+    ids[3, 1] = 8   # out of range: contributes nothing
+    ids[5, 0] = -1
+    y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
+    assert y.dtype == torch.float16
+    xs = x.float().numpy()
+    # fp16 layer oracle: the same composition with fp16 rounding points
+    ones = np.ones(8)
+    gu = O.round_to_dtype(O.fused_moe_fp64(xs, w13, s13, 1.0, ones, w.numpy(), ids.numpy(), False,
+                                           compute_dtype="f16"), "f16")
+    inter = gu.shape[-1] // 2
+    gg, uu = gu[..., :inter], gu[..., inter:]
+    h = O.round_to_dtype(O.round_to_dtype(gg / (1 + np.exp(-gg)), "f16") * uu, "f16")
+    d = O.fused_moe_fp64(h.reshape(m * 2, inter), w2, s2, 1.0, ones, w.numpy().reshape(-1, 1),
+                         ids.numpy().reshape(-1, 1), True, compute_dtype="f16")
+    oracle = O.round_to_dtype(d, "f16")[:, 0].reshape(m, 2, -1).sum(1)
+    t = torch.from_numpy
+    safe = O.moe_layer_safe(x, t(w13), t(s13), t(w2), t(s2), w, ids)
+    assert_layer_parity(y, oracle, safe)

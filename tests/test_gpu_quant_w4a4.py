@@ -1,0 +1,93 @@
+"""GPU parity: the activation quantizer (bit-exact vs the oracle, both
+modes) and W4A4 on the block-scaled FP4 MFMA (tolerance vs FP64)."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import mxfp4_amd as mx
+from oracle import c_oracle, mxfp4_oracle as O
+
+from _helpers import assert_parity, cuda, rand_act, rand_mxfp4
+
+pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::RuntimeWarning")]
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.mark.parametrize("mode", ["ties_away", "rne"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_quant_matches_oracle(mode, dtype):
+    g = torch.Generator().manual_seed(99)
+    x = torch.randn((64, 2048), generator=g) * torch.exp2(torch.randint(-20, 20, (64, 1),
+                                                                           generator=g).float())
+    x[0, :32] = 0.0
+    x[1, :8] = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -5.0])
+    x[2, 3] = -0.0
+    x = x.to(dtype)
+    p, s = mx.dynamic_mxfp4_quant(cuda(x), mode=mode)
+    rp, rs = c_oracle.quant(x.float().numpy(), mode)
+    assert np.array_equal(p.cpu().numpy(), rp) and np.array_equal(s.cpu().numpy(), rs)
+
+
+def test_quant_golden_fixture():
+    g = np.load(os.path.join(GOLDEN, "small_cases.npz"))
+    x = cuda(g["quant_x"])
+    p, s = mx.dynamic_mxfp4_quant(x, "ties_away")
+    assert np.array_equal(p.cpu().numpy(), g["quant_ta_p"])
+    assert np.array_equal(s.cpu().numpy(), g["quant_ta_s"])
+    p, s = mx.dynamic_mxfp4_quant(x, "rne")
+    assert np.array_equal(p.cpu().numpy(), g["quant_rne_p"])
+    assert np.array_equal(s.cpu().numpy(), g["quant_rne_s"])
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 128, 64), (16, 4096, 256), (100, 2080, 300),
+                                   (256, 1024, 512)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_w4a4_linear(m, k, n, out_dtype):
+    rng = np.random.default_rng(m * 31 + n)
+    a = rand_act(m + k, (m, k)).float().numpy()
+    w = (rand_act(n + k, (n, k)).float() * 0.02).numpy()
+    ap, asc = O.quant_mxfp4_rne(a)
+    wp, wsc = O.quant_mxfp4_rne(w)
+    y = mx.linear_mxfp4_w4a4(cuda(ap), cuda(asc), cuda(wp), cuda(wsc), out_dtype)
+    oracle = O.dequant_values(ap, asc, "f32") @ O.dequant_values(wp, wsc, "f32").T
+    assert_parity(y, oracle, what=f"w4a4 {m}x{k}x{n}")
+    del rng
+
+
+def test_w4a4_baseline_shape_sampled():
+    # M=8192, K=4096, N=4096 (checked on sampled rows)
+    m, k, n = 8192, 4096, 4096
+    a = rand_act(4, (m, k))
+    w = rand_act(5, (n, k)).float() * 0.02
+    ap, asc = mx.dynamic_mxfp4_quant(cuda(a), "rne")
+    wp, wsc = mx.dynamic_mxfp4_quant(cuda(w), "rne")
+    y = mx.linear_mxfp4_w4a4(ap, asc, wp, wsc)
+    rows = np.sort(np.random.default_rng(6).choice(m, 64, replace=False))
+    apn, ascn = ap.cpu().numpy()[rows], asc.cpu().numpy()[rows]
+    oracle = O.dequant_values(apn, ascn, "f32") @ O.dequant_values(
+        wp.cpu().numpy(), wsc.cpu().numpy(), "f32").T
+    assert_parity(y[torch.from_numpy(rows).cuda()], oracle)
+
+
+@pytest.mark.parametrize("m", [3, 64])
+def test_w4a4_through_fused_moe(m):
+    rng = np.random.default_rng(m)
+    e, k, n, top_k = 6, 256, 128, 2
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    ap, asc = O.quant_mxfp4_ties_away(rand_act(m, (m, k)).float().numpy())
+    g = torch.Generator().manual_seed(m)
+    w, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
+    C = torch.empty((m, top_k, n), dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4_soft(cuda(ap), cuda(wp), C, torch.tensor([0.75], device="cuda"),
+                            torch.linspace(0.5, 1.25, e, device="cuda"), cuda(asc), cuda(ws),
+                            cuda(w), cuda(ids), torch.empty(0, device="cuda"),
+                            torch.empty(0, device="cuda"), torch.empty(0, device="cuda"), True,
+                            top_k, False, False)
+    oracle = O.fused_moe_fp64(O.dequant_values(ap, asc, "bf16"), wp, ws, 0.75,
+                              np.linspace(0.5, 1.25, e), w.numpy(), ids.numpy(), True)
+    assert_parity(C, oracle)
