@@ -295,7 +295,7 @@ def main() -> int:
                    "activations": "bf16"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "w4a16_tiled<bf16,4,4,STORE>",
+                     "traffic": None, "kernel": "w4a16_pf<bf16> 128x128 tile (direct-to-LDS)",
                      "kernel_us": round(kernel_ms * 1e3, 3),
                      "algorithmic_bytes": linear_bytes(m, n, k)},
     }

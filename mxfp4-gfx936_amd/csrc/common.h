@@ -14,7 +14,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/mxfp4_gfx950.h"
+#include "mxfp4_gfx950.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -37,12 +37,15 @@ int launch_status(const char* what);             // checks hipGetLastError()
 
 // ---------------------------------------------------------------- device side
 
-// E8M0 byte -> the FP32 scale the converter expects.
+// E8M0 byte -> scale operand of v_cvt_scalef32_pk_*_fp4.  The converter
+// reads only the exponent field of that operand (verified on the device for
+// every scale byte x every code pair: a mantissa of 0.5 changes no output
+// bit), so the byte goes straight into the exponent.  The 0x400000 mantissa
+// bit makes s = 0 the subnormal 2^-127 and s = 255 a quiet NaN, the two
+// encodings the converter is known to treat as 2^-127 and NaN.  One
+// v_lshl_or_b32.  The result is only meaningful as the converter's operand.
 __device__ __forceinline__ float e8m0_scale(uint32_t s) {
-  uint32_t bits = s << 23;
-  bits = (s == 0u) ? 0x00400000u : bits;    // 2^-127 is an FP32 subnormal
-  bits = (s == 255u) ? 0x7FC00000u : bits;  // NaN scale -> NaN for every code
-  return __uint_as_float(bits);
+  return __uint_as_float((s << 23) | 0x00400000u);
 }
 
 // Eight E2M1 codes (one dword, low nibble first) times scale -> 8 x T.

@@ -21,6 +21,7 @@ enum Epilogue {
 struct GemmArgs {
   const void* a;        // activations (T) or packed u8
   const uint8_t* a_mx;  // packed A scales [a_rows, k/32] (W4A4 only)
+  int64_t a_rows;       // activation rows addressable through `a`
   int64_t lda;          // A row stride, elements (bytes for packed A)
   int64_t lda_mx;       // A scale row stride, bytes
   const uint8_t* b;     // packed weights, expert-major
@@ -82,6 +83,11 @@ __device__ __forceinline__ float scalar_alpha(const GemmArgs& g, int expert) {
 
 // Host-side launchers (gemm_w4a16.hip, gemm_w4a4.hip).
 int launch_w4a16(const GemmArgs& g, int dtype, int epi, hipStream_t st);
+// Direct-to-LDS prefill kernel (gemm_w4a16_pf.hip): tile configurations.
+enum PfConfig { PF_128x256 = 0, PF_128x128 = 1, PF_64x128 = 2, PF_32x128 = 3 };
+bool pf_supported(const GemmArgs& g, int elem_bytes);
+int pf_choose(const GemmArgs& g, int epi);
+int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t st);
 int launch_w4a4(const GemmArgs& g, int out_dtype, hipStream_t st);
 int launch_f32_reference(const GemmArgs& g, int a_dtype, hipStream_t st);
 

@@ -21,6 +21,8 @@
 //
 // The SiLU*mul epilogue (vllm:249-252) pairs gate column j with up column
 // inter + j inside the same lane, so the gate_up GEMM writes h directly.
+#include <type_traits>
+
 #include "gemm.h"
 
 namespace mx {
@@ -405,8 +407,10 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
       w4a16_skinny<T, 2, 8, EPI><<<grid, 512, 0, st>>>(g);
     return launch_status("w4a16 skinny launch");
   }
-  // tiled: BM must divide block_m (routed); pick the largest BM that still
-  // gives >= 512 workgroups, else the smallest.
+  const int dt = std::is_same<T, __bf16>::value ? MXFP4_DT_BF16 : MXFP4_DT_F16;
+  if (pf_supported(g, (int)sizeof(T))) return launch_w4a16_pf(g, dt, EPI, pf_choose(g, EPI), st);
+  // register-staged kernel: BM must divide block_m (routed); the largest BM
+  // that still gives >= 512 workgroups, else the smallest
   const int tile_cols = (EPI == EPI_SILU_MUL) ? 64 : 128;
   const int64_t ntiles = (out_cols + tile_cols - 1) / tile_cols;
   int bm = 32;

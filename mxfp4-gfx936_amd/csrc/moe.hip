@@ -333,6 +333,7 @@ extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_
   GemmArgs g = {};
   g.a = a;
   g.a_mx = a_mx;
+  g.a_rows = a_rows;
   g.lda = a_row_stride;
   g.lda_mx = k / 32;
   g.b = b;
@@ -355,7 +356,6 @@ extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_
   g.k = (int32_t)k;
   g.top_k = top_k;
   g.block_m = block_m;
-  (void)a_rows;
   return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, static_cast<hipStream_t>(stream));
 }
 
@@ -382,6 +382,7 @@ extern "C" int mxfp4_linear_w4a16(const void* x, int x_dtype, int64_t m, int64_t
   if (m == 0) return MXFP4_OK;
   GemmArgs g = {};
   g.a = x;
+  g.a_rows = m;
   g.lda = x_row_stride;
   g.b = packed;
   g.bs = scales;
@@ -418,6 +419,7 @@ extern "C" int mxfp4_linear_w4a4(const uint8_t* a, const uint8_t* a_mx, int64_t 
   GemmArgs g = {};
   g.a = a;
   g.a_mx = a_mx;
+  g.a_rows = m;
   g.lda = k / 2;
   g.lda_mx = k / 32;
   g.b = b;
@@ -491,6 +493,7 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
   // gate_up with the fused SiLU*mul epilogue: h[r, :inter]
   GemmArgs g = {};
   g.a = x;
+  g.a_rows = m;
   g.lda = hidden;
   g.b = w13;
   g.bs = s13;
@@ -516,6 +519,7 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
   // down with the route weight: d[r, :hidden]
   GemmArgs g2 = g;
   g2.a = h;
+  g2.a_rows = p.routes;
   g2.lda = inter;
   g2.b = w2;
   g2.bs = s2;
