@@ -130,9 +130,11 @@ int mxfp4_moe_align(const void* topk_ids, int ids_dtype, int64_t num_routes, int
  *   e = expert_ids[i] and each route r = sorted_ids[i*block_m + j] <
  *   num_valid:  c[r, :] = a[r / top_k] . dequant(b[e])^T * a_scale[0] *
  *   b_scale[e] (* topk_weights[r] if mul_routed_weight), rounded once to
- *   c_dtype.  Expert -1 writes zeros (aiter:156-172).  Rows not named by
- *   the metadata are not written.  a_scale / b_scale may be NULL (= 1).
- *   block_m % 16 == 0; k % 32 == 0; em = capacity of sorted_ids.
+ *   c_dtype.  Expert -1 writes zeros (aiter:156-172); so does any other id
+ *   outside [0, num_experts).  Rows not named by the metadata are not
+ *   written.  a_scale / b_scale may be NULL (= 1).  block_m % 16 == 0;
+ *   k % 32 == 0; em = capacity of sorted_ids; expert_ids holds em / block_m
+ *   entries, any of which may be read.
  */
 int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
                    const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,

@@ -24,6 +24,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
@@ -44,6 +45,38 @@ int launch_status(const char* what);             // checks hipGetLastError()
 // bit makes s = 0 the subnormal 2^-127 and s = 255 a quiet NaN, the two
 // encodings the converter is known to treat as 2^-127 and NaN.  One
 // v_lshl_or_b32.  The result is only meaningful as the converter's operand.
+// Raw (MUBUF) buffer loads through a 128-bit resource {base, byte size,
+// raw-buffer flags}: a lane whose byte offset lies at or past the size reads
+// zero instead of memory.  Kernels use kOOB for padding rows and K tails,
+// so their loads need no branches; every resource they build is at most
+// 2 GiB, which keeps kOOB out of range.
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ i32x4 make_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return i32x4{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
+}
+
+extern "C" __device__ i32x4 llvm_amdgcn_raw_buffer_load_v4i32(i32x4 rsrc, uint32_t voffset,
+                                                               int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+extern "C" __device__ i32x2 llvm_amdgcn_raw_buffer_load_v2i32(i32x4 rsrc, uint32_t voffset,
+                                                               int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v2i32");
+extern "C" __device__ uint8_t llvm_amdgcn_raw_buffer_load_i8(i32x4 rsrc, uint32_t voffset,
+                                                             int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i8");
+
+__device__ __forceinline__ i32x4 buf_load16(i32x4 rsrc, uint32_t off) {
+  return llvm_amdgcn_raw_buffer_load_v4i32(rsrc, off, 0, 0);
+}
+__device__ __forceinline__ i32x2 buf_load8(i32x4 rsrc, uint32_t off) {
+  return llvm_amdgcn_raw_buffer_load_v2i32(rsrc, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load_u8(i32x4 rsrc, uint32_t off) {
+  return llvm_amdgcn_raw_buffer_load_i8(rsrc, off, 0, 0);
+}
+
 __device__ __forceinline__ float e8m0_scale(uint32_t s) {
   return __uint_as_float((s << 23) | 0x00400000u);
 }

@@ -44,6 +44,7 @@ struct GemmArgs {
   int32_t top_k;      // activation row = route / top_k
   int32_t block_m;    // rows per expert block in sorted_ids
   int32_t inter;      // SiLU epilogue: row offset of the `up` half in B
+  int32_t num_experts;  // routed: experts in b; other expert ids act as -1
 };
 
 // Per-row routing lookup used by every kernel.
@@ -66,6 +67,14 @@ __device__ __forceinline__ RowInfo row_info(const GemmArgs& g, int64_t pos) {
     ri.a_row = ri.valid ? (r / g.top_k) : 0;
   }
   return ri;
+}
+
+// Expert of the routed block holding padded position `pos`; ids outside
+// [0, num_experts) are treated as -1 (zeros) instead of addressing memory
+// beyond the weights.
+__device__ __forceinline__ int block_expert(const GemmArgs& g, int64_t pos) {
+  const int e = g.expert_ids[pos / g.block_m];
+  return (e >= 0 && e < g.num_experts) ? e : -1;
 }
 
 // Number of padded rows in use (routed: read from the device scalar).

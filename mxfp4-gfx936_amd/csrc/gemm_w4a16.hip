@@ -21,6 +21,7 @@
 //
 // The SiLU*mul epilogue (vllm:249-252) pairs gate column j with up column
 // inter + j inside the same lane, so the gate_up GEMM writes h directly.
+#include <algorithm>
 #include <type_traits>
 
 #include "gemm.h"
@@ -65,81 +66,147 @@ __device__ __forceinline__ void store_out(const GemmArgs& g, const RowInfo& r, i
 }
 
 // ---------------------------------------------------------------- skinny
-template <typename T, int RB, int NW, int EPI>
-__global__ __launch_bounds__(NW * 64) void w4a16_skinny(GemmArgs g) {
+// NW = WK x WN waves.  Each wave owns CG adjacent groups of 16 output
+// columns (for SiLU each group is a gate block and an up block) and one of
+// WK slices of K; WN such waves sit side by side on columns.  Loads are
+// what bounds this kernel (each vector memory instruction costs the
+// address unit about the same, however few lanes it has active), so a wave
+// reuses each activation fragment for its CG column groups, and takes the
+// scales of a whole trip with one load per column block.  A wave takes U
+// consecutive 128-K units per trip and issues every load of the trip
+// before its first MFMA; all loads are branch-free buffer loads (zero past
+// the end) except the activation loads of padding rows, which are
+// exec-masked off.  Routed blocks read the block's expert id and the padded
+// row count with two independent scalar loads.
+template <typename T, int RB, int WK, int WN, int CG, int U, int EPI>
+__global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
   typedef typename V8Of<T>::type V8;
   constexpr int CB = (EPI == EPI_SILU_MUL) ? 2 : 1;
-  __shared__ f32x4 red[NW][RB * CB][64];
+  constexpr int NB = CB * CG;  // weight blocks of 16 rows per wave
+  static_assert(U == 2 || U == 4, "scale loads cover 2 or 4 units");
+  __shared__ f32x4 red[WK][WN * CG][RB * CB][64];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int wk = wave % WK;
+  const int wn = wave / WK;
   const int c16 = lane & 15;
   const int grp = lane >> 4;
   const int64_t pos0 = (int64_t)blockIdx.y * (16 * RB);
-  if (pos0 >= rows_in_use(g)) return;
-  const int expert = g.sorted_ids ? g.expert_ids[pos0 / g.block_m] : 0;
-  const int n0 = blockIdx.x * 16;
+  int expert = 0;
+  if (g.sorted_ids) {
+    const int64_t npp = *g.num_post_padded;
+    const int e = block_expert(g, pos0);
+    if (pos0 >= (npp < g.m ? npp : g.m)) return;
+    expert = e;
+  } else if (pos0 >= g.m) {
+    return;
+  }
+  const int n0 = (blockIdx.x * WN + wn) * 16 * CG;
 
-  f32x4 acc[RB][CB];
+  f32x4 acc[RB][NB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < NB; ++nb) acc[rb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (expert >= 0) {
-    const int col = n0 + c16;
-    const bool col_ok = col < g.n;
-    const uint8_t* bp[CB];
-    const uint8_t* sp[CB];
+    // Buffer resources: this expert's weights and scales, and the whole
+    // activation matrix (host-checked to stay below 2 GiB each).  Columns
+    // past N re-read row 0 (their outputs are not stored); padding rows
+    // and K past the end read zeros through kOOB.
+    const int64_t b_rows_total = (CB == 2) ? 2 * (int64_t)g.inter : (int64_t)g.n;
+    const i32x4 rB = make_rsrc(g.b + expert * g.b_e, (uint32_t)(b_rows_total * g.b_n));
+    const i32x4 rS = make_rsrc(g.bs + expert * g.bs_e, (uint32_t)(b_rows_total * g.bs_n));
+    const i32x4 rA = make_rsrc(g.a, (uint32_t)(g.a_rows * g.lda * (int64_t)sizeof(T)));
+    uint32_t boff[NB], soff[NB];
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const int64_t brow = (cb == 0 ? 0 : g.inter) + (col_ok ? col : 0);
-      bp[cb] = g.b + expert * g.b_e + brow * g.b_n;
-      sp[cb] = g.bs + expert * g.bs_e + brow * g.bs_n;
+    for (int nb = 0; nb < NB; ++nb) {
+      const int col = n0 + (nb / CB) * 16 + c16;
+      const int64_t brow = ((nb % CB) == 0 ? 0 : g.inter) + (col < g.n ? col : 0);
+      boff[nb] = (uint32_t)(brow * g.b_n);
+      soff[nb] = (uint32_t)(brow * g.bs_n);
     }
-    const T* ap[RB];
-    bool a_ok[RB];
+    uint32_t aoff[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const RowInfo ri = row_info(g, pos0 + rb * 16 + c16);
-      a_ok[rb] = ri.valid;
-      ap[rb] = static_cast<const T*>(g.a) + ri.a_row * g.lda;
+      aoff[rb] = ri.valid ? (uint32_t)(ri.a_row * g.lda * (int64_t)sizeof(T)) : kOOB;
     }
     const int nunits = (g.k + 127) >> 7;
-    for (int u = wave; u < nunits; u += NW) {
-      const int k0 = u * 128 + grp * 32;
-      const bool k_ok = k0 < g.k;
-      i32x4 braw[CB];
-      float bsc[CB];
+    // buffer dword loads need 4-byte aligned addresses
+    const bool s_dword = ((g.bs_n | g.bs_e | (int64_t)reinterpret_cast<uintptr_t>(g.bs)) & 3) == 0;
+    const uint32_t sshift = s_dword ? 8u * grp : 0u;
+    for (int u0 = wk * U; u0 < nunits; u0 += WK * U) {
+      // Scales: with 4-byte aligned scale rows one load per lane and weight
+      // block covers the trip -- the U x 4 E8M0 bytes of its row (4 per
+      // unit, one per lane group), lane group grp taking byte grp of each
+      // unit's dword; otherwise one byte load per unit.  Bytes are
+      // extracted where they are used, so no load result is consumed here.
+      uint32_t sdw[NB][U];
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        if (col_ok && k_ok) {
-          braw[cb] = *reinterpret_cast<const i32x4*>(bp[cb] + (k0 >> 1));
-          bsc[cb] = e8m0_scale(sp[cb][k0 >> 5]);
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t so = soff[nb] + (uint32_t)(u0 * 4);
+        if (s_dword) {
+          if (U == 4) {
+            const i32x4 v = buf_load16(rS, so);
+#pragma unroll
+            for (int uu = 0; uu < U; ++uu) sdw[nb][uu] = (uint32_t)v[uu];
+          } else {
+            const i32x2 v = buf_load8(rS, so);
+#pragma unroll
+            for (int uu = 0; uu < U; ++uu) sdw[nb][uu] = (uint32_t)v[uu];
+          }
         } else {
-          braw[cb] = i32x4{0, 0, 0, 0};
-          bsc[cb] = 1.0f;
+#pragma unroll
+          for (int uu = 0; uu < U; ++uu) sdw[nb][uu] = buf_load_u8(rS, so + 4 * uu + grp);
         }
       }
-      V8 af[RB][4];
+      i32x4 braw[U][NB];
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        if (a_ok[rb] && k_ok) {
-          const V8* src = reinterpret_cast<const V8*>(ap[rb] + k0);
+      for (int uu = 0; uu < U; ++uu) {
+        const int k0 = (u0 + uu) * 128 + grp * 32;
+        const bool k_ok = k0 < g.k;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) af[rb][j] = src[j];
-        } else {
+        for (int nb = 0; nb < NB; ++nb)
+          braw[uu][nb] = buf_load16(rB, k_ok ? boff[nb] + (uint32_t)(k0 >> 1) : kOOB);
+      }
+      V8 af[U][RB][4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) af[rb][j] = zero_v8<V8>();
+      for (int uu = 0; uu < U; ++uu) {
+        const int k0 = (u0 + uu) * 128 + grp * 32;
+        const bool k_ok = k0 < g.k;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          // nothing in this branch consumes the loaded values, so no wait
+          // is placed in it
+          if (k_ok && aoff[rb] != kOOB) {
+            const uint32_t o = aoff[rb] + (uint32_t)(k0 * (int)sizeof(T));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              af[uu][rb][j] = __builtin_bit_cast(V8, buf_load16(rA, o + 16 * j));
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) af[uu][rb][j] = zero_v8<V8>();
+          }
         }
       }
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
+      for (int uu = 0; uu < U; ++uu) {
+        // K past the end: weights read as zero; the scale is forced to 1 so
+        // bytes of the next row (possibly NaN) cannot leak in
+        const bool k_ok = (u0 + uu) * 128 + grp * 32 < g.k;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const V8 bf = Decode<T>::run((uint32_t)braw[cb][j], bsc[cb]);
+        for (int nb = 0; nb < NB; ++nb) {
+          const uint32_t sb = k_ok ? (sdw[nb][uu] >> sshift) & 0xFFu : 127u;
+          const float sc = e8m0_scale(sb);
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) acc[rb][cb] = mfma16(af[rb][j], bf, acc[rb][cb]);
+          for (int j = 0; j < 4; ++j) {
+            const V8 bf = Decode<T>::run((uint32_t)braw[uu][nb][j], sc);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+              acc[rb][nb] = mfma16(af[uu][rb][j], bf, acc[rb][nb]);
+          }
         }
       }
     }
@@ -148,15 +215,17 @@ __global__ __launch_bounds__(NW * 64) void w4a16_skinny(GemmArgs g) {
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) red[wave][rb * CB + cb][lane] = acc[rb][cb];
+    for (int nb = 0; nb < NB; ++nb)
+      red[wk][wn * CG + nb / CB][rb * CB + nb % CB][lane] = acc[rb][nb];
   __syncthreads();
 
   const float alpha = expert >= 0 ? scalar_alpha(g, expert) : 0.f;
-  for (int idx = threadIdx.x; idx < RB * 256; idx += NW * 64) {
-    const int rb = idx >> 8;
+  for (int idx = threadIdx.x; idx < WN * CG * RB * 256; idx += WK * WN * 64) {
+    const int cgi = idx / (RB * 256);
+    const int rb = (idx >> 8) % RB;
     const int l = (idx >> 2) & 63;
     const int i = idx & 3;
-    const int col = n0 + (l & 15);
+    const int col = (blockIdx.x * WN * CG + cgi) * 16 + (l & 15);
     const RowInfo r = row_info(g, pos0 + rb * 16 + (l >> 4) * 4 + i);
     if (!r.valid || col >= g.n) continue;
     if (expert < 0) {
@@ -168,7 +237,7 @@ __global__ __launch_bounds__(NW * 64) void w4a16_skinny(GemmArgs g) {
     for (int cb = 0; cb < CB; ++cb) {
       float s = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) s += red[w][rb * CB + cb][l][i];
+      for (int w = 0; w < WK; ++w) s += red[w][cgi][rb * CB + cb][l][i];
       v[cb] = s;
     }
     store_out<T, EPI>(g, r, col, alpha, v[0], v[CB - 1]);
@@ -203,7 +272,7 @@ __global__ __launch_bounds__(256) void w4a16_tiled(GemmArgs g) {
 
   const int64_t pos0 = (int64_t)blockIdx.y * BM;
   if (pos0 >= rows_in_use(g)) return;
-  const int expert = g.sorted_ids ? g.expert_ids[pos0 / g.block_m] : 0;
+  const int expert = g.sorted_ids ? block_expert(g, pos0) : 0;
   const int ncol0 = blockIdx.x * OUT_COLS;
 
   if (expert < 0) {  // aiter:156-172: expert not on this device -> zeros
@@ -356,7 +425,7 @@ __global__ __launch_bounds__(256) void f32_gemm(GemmArgs g) {
   for (int64_t pos = blockIdx.y; pos < used; pos += gridDim.y) {
     const RowInfo r = row_info(g, pos);
     if (!r.valid || col >= g.n) continue;
-    const int expert = g.sorted_ids ? g.expert_ids[pos / g.block_m] : 0;
+    const int expert = g.sorted_ids ? block_expert(g, pos) : 0;
     float* cp = static_cast<float*>(g.c) + r.out_row * g.ldc + col;
     if (expert < 0) {
       *cp = 0.f;
@@ -379,6 +448,51 @@ __global__ __launch_bounds__(256) void f32_gemm(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------- dispatch
+// Wave layout for the skinny kernel: the fewest K-splitting waves WK whose
+// single trip (WK x U units of 128) covers K, the rest of the 4 waves side
+// by side on columns (8 K-splitting waves beyond 4 x U units).  For short
+// K (at most 2 K-splitting waves) each wave takes two column groups
+// (CG = 2) once the grid would otherwise hold more than 4 workgroups per
+// CU; for longer K the extra registers cost more occupancy than the shared
+// activation loads save (measured on the MoE decode shapes).
+struct SkinnyShape {
+  int rb, wk, wn, cg, u;
+};
+
+SkinnyShape skinny_shape(int64_t k, int64_t n, int64_t row_blocks, int rb) {
+  const int64_t units = (k + 127) / 128;
+  SkinnyShape s;
+  s.rb = rb;
+  s.u = rb == 1 ? 4 : 2;
+  s.wk = 8;
+  for (int wk = 1; wk <= 4; wk *= 2)
+    if ((int64_t)wk * s.u >= units) {
+      s.wk = wk;
+      break;
+    }
+  s.wn = s.wk >= 4 ? 1 : 4 / s.wk;
+  const int64_t wgs = (n + 16 * s.wn - 1) / (16 * s.wn) * row_blocks;
+  s.cg = (wgs > 4 * 256 && s.wk <= 2) ? 2 : 1;
+  return s;
+}
+
+template <typename T, int RB, int CG, int EPI>
+void skinny_launch_cg(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStream_t st) {
+  constexpr int U = RB == 1 ? 4 : 2;
+  switch (s.wk) {
+    case 1: w4a16_skinny<T, RB, 1, 4, CG, U, EPI><<<grid, 256, 0, st>>>(g); break;
+    case 2: w4a16_skinny<T, RB, 2, 2, CG, U, EPI><<<grid, 256, 0, st>>>(g); break;
+    case 4: w4a16_skinny<T, RB, 4, 1, CG, U, EPI><<<grid, 256, 0, st>>>(g); break;
+    default: w4a16_skinny<T, RB, 8, 1, CG, U, EPI><<<grid, 512, 0, st>>>(g); break;
+  }
+}
+
+template <typename T, int RB, int EPI>
+void skinny_launch_rb(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStream_t st) {
+  if (s.cg == 2) skinny_launch_cg<T, RB, 2, EPI>(g, s, grid, st);
+  else skinny_launch_cg<T, RB, 1, EPI>(g, s, grid, st);
+}
+
 template <typename T, int EPI>
 int launch_typed(const GemmArgs& g, hipStream_t st) {
   const int64_t cap = g.m;  // dense rows or sorted capacity
@@ -393,6 +507,19 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
   } else if (cap <= 32) {
     skinny_rb = cap <= 16 ? 1 : 2;
   }
+  // the skinny kernel addresses its operands through 2 GiB buffer
+  // resources; larger operands go to the tiled kernel where the block size
+  // allows it
+  const int64_t b_rows_total = (EPI == EPI_SILU_MUL) ? 2 * (int64_t)g.inter : (int64_t)g.n;
+  const int64_t lim = 0x7FFFFFFF;
+  if (skinny_rb && (g.a_rows * g.lda * (int64_t)sizeof(T) > lim || b_rows_total * g.b_n > lim ||
+                    b_rows_total * g.bs_n > lim)) {
+    if (routed && g.block_m % 32 != 0) {
+      set_error("w4a16: operands above 2 GiB need a routing block size that is a multiple of 32");
+      return MXFP4_ERR_VALUE;
+    }
+    skinny_rb = 0;
+  }
   if (skinny_rb) {
     const int rb = skinny_rb;
     const int64_t gy = (cap + 16 * rb - 1) / (16 * rb);
@@ -400,11 +527,17 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
       set_error("w4a16: too many row blocks (%lld)", (long long)gy);
       return MXFP4_ERR_VALUE;
     }
-    dim3 grid((out_cols + 15) / 16, (unsigned)(gy > 0 ? gy : 1));
+    // active row blocks: dense rows, or at most one partial block per
+    // routed expert plus the full ones
+    const int64_t blocks = routed ? std::min<int64_t>(gy, g.num_valid / (16 * rb) + g.num_experts)
+                                  : gy;
+    const SkinnyShape sh = skinny_shape(g.k, out_cols, blocks, rb);
+    const int tile_cols = 16 * sh.wn * sh.cg;
+    dim3 grid((unsigned)((out_cols + tile_cols - 1) / tile_cols), (unsigned)(gy > 0 ? gy : 1));
     if (rb == 1)
-      w4a16_skinny<T, 1, 8, EPI><<<grid, 512, 0, st>>>(g);
+      skinny_launch_rb<T, 1, EPI>(g, sh, grid, st);
     else
-      w4a16_skinny<T, 2, 8, EPI><<<grid, 512, 0, st>>>(g);
+      skinny_launch_rb<T, 2, EPI>(g, sh, grid, st);
     return launch_status("w4a16 skinny launch");
   }
   const int dt = std::is_same<T, __bf16>::value ? MXFP4_DT_BF16 : MXFP4_DT_F16;

@@ -41,12 +41,6 @@ extern "C" __device__ void llvm_amdgcn_raw_buffer_load_lds(i32x4 rsrc, lds_u32* 
                                                            int aux)
     __asm("llvm.amdgcn.raw.buffer.load.lds");
 
-constexpr uint32_t kOOB = 0x80000000u;  // offset past every buffer: reads as zero
-
-__device__ __forceinline__ i32x4 make_rsrc(const void* p, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(p);
-  return i32x4{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
-}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -123,7 +117,7 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int n
 
   const int64_t pos0 = (int64_t)bm * BM;
   if (pos0 >= rows_in_use(g)) return;
-  const int expert = g.sorted_ids ? g.expert_ids[pos0 / g.block_m] : 0;
+  const int expert = g.sorted_ids ? block_expert(g, pos0) : 0;
   const int ncol0 = bn * OUT_COLS;
 
   if (expert < 0) {  // aiter:156-172: expert not on this device -> zeros

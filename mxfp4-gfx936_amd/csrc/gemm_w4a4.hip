@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
 
   const int64_t pos0 = (int64_t)blockIdx.y * BM;
   if (pos0 >= rows_in_use(g)) return;
-  const int expert = g.sorted_ids ? g.expert_ids[pos0 / g.block_m] : 0;
+  const int expert = g.sorted_ids ? block_expert(g, pos0) : 0;
   const int ncol0 = blockIdx.x * BN;
 
   if (expert < 0) {

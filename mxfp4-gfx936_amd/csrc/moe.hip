@@ -356,6 +356,7 @@ extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_
   g.k = (int32_t)k;
   g.top_k = top_k;
   g.block_m = block_m;
+  g.num_experts = (int32_t)num_experts;
   return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, static_cast<hipStream_t>(stream));
 }
 
@@ -513,6 +514,7 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
   g.top_k = top_k;
   g.block_m = p.block_m;
   g.inter = (int32_t)inter;
+  g.num_experts = num_experts;
   rc = launch_w4a16(g, x_dtype, EPI_SILU_MUL, st);
   if (rc) return rc;
 
