@@ -63,6 +63,9 @@ extern "C" __device__ i32x4 llvm_amdgcn_raw_buffer_load_v4i32(i32x4 rsrc, uint32
 extern "C" __device__ i32x2 llvm_amdgcn_raw_buffer_load_v2i32(i32x4 rsrc, uint32_t voffset,
                                                                int soffset, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.v2i32");
+extern "C" __device__ int llvm_amdgcn_raw_buffer_load_i32(i32x4 rsrc, uint32_t voffset,
+                                                           int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i32");
 extern "C" __device__ uint8_t llvm_amdgcn_raw_buffer_load_i8(i32x4 rsrc, uint32_t voffset,
                                                              int soffset, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.i8");
@@ -73,8 +76,31 @@ __device__ __forceinline__ i32x4 buf_load16(i32x4 rsrc, uint32_t off) {
 __device__ __forceinline__ i32x2 buf_load8(i32x4 rsrc, uint32_t off) {
   return llvm_amdgcn_raw_buffer_load_v2i32(rsrc, off, 0, 0);
 }
+__device__ __forceinline__ uint32_t buf_load4(i32x4 rsrc, uint32_t off) {
+  return (uint32_t)llvm_amdgcn_raw_buffer_load_i32(rsrc, off, 0, 0);
+}
 __device__ __forceinline__ uint32_t buf_load_u8(i32x4 rsrc, uint32_t off) {
   return llvm_amdgcn_raw_buffer_load_i8(rsrc, off, 0, 0);
+}
+
+// Direct-to-LDS buffer loads: each lane's `size` bytes land at the wave's
+// LDS base (taken from M0) + size x lane, without passing through VGPRs.
+// The compiler does not order later LDS reads after these writes: callers
+// wait with wait_vmcnt and a barrier.
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+
+extern "C" __device__ void llvm_amdgcn_raw_buffer_load_lds(i32x4 rsrc, lds_u32* lds, int size,
+                                                           int voffset, int soffset, int offset,
+                                                           int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ lds_u32* lds_ptr(uint8_t* p) {
+  return (lds_u32*)(__attribute__((address_space(3))) uint8_t*)p;
 }
 
 __device__ __forceinline__ float e8m0_scale(uint32_t s) {

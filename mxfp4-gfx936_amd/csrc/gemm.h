@@ -45,6 +45,12 @@ struct GemmArgs {
   int32_t block_m;    // rows per expert block in sorted_ids
   int32_t inter;      // SiLU epilogue: row offset of the `up` half in B
   int32_t num_experts;  // routed: experts in b; other expert ids act as -1
+  // Direct routing (skinny kernel, 16-row blocks): instead of sorted
+  // metadata, the top-k ids themselves ([num_valid], int32 or int64).
+  // Workgroup row r handles route r if it is the 0th, 16th, ... route of
+  // its expert, together with the next 15 routes of that expert.
+  const void* route_ids;
+  int32_t ids64;
 };
 
 // Per-row routing lookup used by every kernel.
@@ -99,5 +105,11 @@ int pf_choose(const GemmArgs& g, int epi);
 int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t st);
 int launch_w4a4(const GemmArgs& g, int out_dtype, hipStream_t st);
 int launch_f32_reference(const GemmArgs& g, int a_dtype, hipStream_t st);
+// MoE decode: down projection fused with the top-k combine (moe_decode.hip);
+// h holds the m * top_k routes' rows of width inter in route order.
+int launch_moe_down_topk(const void* h, const uint8_t* w2, const uint8_t* s2,
+                         const float* topk_weights, const void* topk_ids, int ids64, int64_t m,
+                         int top_k, int64_t hidden, int64_t inter, int num_experts, void* out,
+                         int dtype, hipStream_t st);
 
 }  // namespace mx

@@ -65,6 +65,91 @@ __device__ __forceinline__ void store_out(const GemmArgs& g, const RowInfo& r, i
   }
 }
 
+// ---------------------------------------------------------------- direct routing
+constexpr int kDirectMaxRoutes = 256;  // routes scanned by one wave (4 x 64)
+
+// Rows of workgroup row r under direct routing: r leads if its expert e is
+// valid and r is the 0th, 16th, 32nd ... route of e (in route order); it
+// then owns that route and the next 15 routes of e.  Every wave finds this
+// on its own from ballots over all route ids (at most kDirectMaxRoutes,
+// loaded as raw words first so no load waits for another), so no barrier
+// is needed.  Returns nonzero if the workgroup has no work.
+template <int RB>
+__device__ __forceinline__ int direct_rows(const GemmArgs& g, int r, int c16, int* expert,
+                                           int64_t* my_route) {
+  static_assert(RB == 1, "direct routing uses 16-row blocks");
+  constexpr int NC = kDirectMaxRoutes / 64;
+  const int lane = threadIdx.x & 63;
+  const int nr = (int)g.num_valid;
+  const int esz = g.ids64 ? 8 : 4;
+  const i32x4 rI = make_rsrc(g.route_ids, (uint32_t)(nr * esz));
+  uint32_t lo[NC], hi[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t off = (uint32_t)((c * 64 + lane) * esz);
+    if (g.ids64) {
+      const i32x2 v = buf_load8(rI, off);
+      lo[c] = (uint32_t)v[0];
+      hi[c] = (uint32_t)v[1];
+    } else {
+      lo[c] = buf_load4(rI, off);
+      hi[c] = 0;
+    }
+  }
+  int64_t id[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t v =
+        g.ids64 ? (int64_t)(((uint64_t)hi[c] << 32) | lo[c]) : (int64_t)(int32_t)lo[c];
+    id[c] = c * 64 + lane < nr ? v : -1;
+  }
+  const int rchunk = r >> 6;
+  int64_t e = -1;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c == rchunk) {
+      const uint32_t elo = __builtin_amdgcn_readlane((int)(uint32_t)id[c], r & 63);
+      const uint32_t ehi =
+          __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)id[c] >> 32), r & 63);
+      e = (int64_t)(((uint64_t)ehi << 32) | elo);
+    }
+  }
+  if (e < 0 || e >= g.num_experts) return 1;
+  int rank = 0, got = 0;
+  my_route[0] = -1;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c * 64 >= nr) break;
+    uint64_t mk = __ballot(id[c] == e);
+    if (c < rchunk) {
+      rank += __popcll(mk);
+      continue;
+    }
+    if (c == rchunk) {
+      const uint64_t below = (1ull << (r & 63)) - 1;
+      rank += __popcll(mk & below);
+      if (rank & 15) return 1;
+      mk &= ~below;
+    }
+    while (mk && got < 16) {
+      const int b = __builtin_ctzll(mk);
+      mk &= mk - 1;
+      if (c16 == got) my_route[0] = c * 64 + b;
+      ++got;
+    }
+  }
+  *expert = (int)e;
+  return 0;
+}
+
+// Activation rows the skinny kernel stages in LDS, and their LDS row
+// stride for K = 128 x nunits (whole 1 KB pieces plus 16 bytes, so rows
+// start on different banks).
+constexpr int kStageRows = 4;
+__host__ __device__ __forceinline__ int stage_stride(int nunits) {
+  return (nunits * 256 + 1023) / 1024 * 1024 + 16;
+}
+
 // ---------------------------------------------------------------- skinny
 // NW = WK x WN waves.  Each wave owns CG adjacent groups of 16 output
 // columns (for SiLU each group is a gate block and an up block) and one of
@@ -85,6 +170,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
   constexpr int NB = CB * CG;  // weight blocks of 16 rows per wave
   static_assert(U == 2 || U == 4, "scale loads cover 2 or 4 units");
   __shared__ f32x4 red[WK][WN * CG][RB * CB][64];
+  extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // staged activation rows
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -93,14 +179,36 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
   const int c16 = lane & 15;
   const int grp = lane >> 4;
   const int64_t pos0 = (int64_t)blockIdx.y * (16 * RB);
+  __shared__ int64_t srow[RB * 16];  // output row of each tile row, -1 = none
   int expert = 0;
-  if (g.sorted_ids) {
+  int64_t my_route[RB];  // output row of this lane's tile row (c16) per row block
+  if (g.route_ids) {
+    if constexpr (RB == 1) {
+      if (direct_rows<RB>(g, (int)blockIdx.y, c16, &expert, my_route)) return;
+    } else {
+      return;  // direct routing is launched with 16-row blocks only
+    }
+  } else if (g.sorted_ids) {
     const int64_t npp = *g.num_post_padded;
     const int e = block_expert(g, pos0);
     if (pos0 >= (npp < g.m ? npp : g.m)) return;
     expert = e;
-  } else if (pos0 >= g.m) {
-    return;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const RowInfo ri = row_info(g, pos0 + rb * 16 + c16);
+      my_route[rb] = ri.valid ? ri.out_row : -1;
+    }
+  } else {
+    if (pos0 >= g.m) return;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int64_t p = pos0 + rb * 16 + c16;
+      my_route[rb] = p < g.m ? p : -1;
+    }
+  }
+  if (wave == 0 && grp == 0) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) srow[rb * 16 + c16] = my_route[rb];
   }
   const int n0 = (blockIdx.x * WN + wn) * 16 * CG;
 
@@ -130,14 +238,24 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
     uint32_t aoff[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const RowInfo ri = row_info(g, pos0 + rb * 16 + c16);
-      aoff[rb] = ri.valid ? (uint32_t)(ri.a_row * g.lda * (int64_t)sizeof(T)) : kOOB;
+      const int64_t arow = (g.sorted_ids || g.route_ids) ? my_route[rb] / g.top_k : my_route[rb];
+      aoff[rb] = my_route[rb] >= 0 ? (uint32_t)(arow * g.lda * (int64_t)sizeof(T)) : kOOB;
     }
     const int nunits = (g.k + 127) >> 7;
     // buffer dword loads need 4-byte aligned addresses
     const bool s_dword = ((g.bs_n | g.bs_e | (int64_t)reinterpret_cast<uintptr_t>(g.bs)) & 3) == 0;
     const uint32_t sshift = s_dword ? 8u * grp : 0u;
-    for (int u0 = wk * U; u0 < nunits; u0 += WK * U) {
+    // Activation staging: when one trip covers K, block rows
+    // 0 .. kStageRows-1 are copied once per workgroup into LDS with
+    // direct-to-LDS loads (1 KB per instruction, all lanes active) instead
+    // of 16 lane-masked loads per wave; other rows load per lane.  The
+    // copies are issued after the weight loads, which do not wait for the
+    // row ids they need.
+    const bool stage = nunits <= WK * U;
+    const int a_stride = stage_stride(nunits);
+    const int trips = stage ? 1 : (nunits - wk * U + WK * U - 1) / (WK * U);
+    for (int t = 0; t < trips; ++t) {
+      const int u0 = wk * U + t * WK * U;
       // Scales: with 4-byte aligned scale rows one load per lane and weight
       // block covers the trip -- the U x 4 E8M0 bytes of its row (4 per
       // unit, one per lane group), lane group grp taking byte grp of each
@@ -171,6 +289,21 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
         for (int nb = 0; nb < NB; ++nb)
           braw[uu][nb] = buf_load16(rB, k_ok ? boff[nb] + (uint32_t)(k0 >> 1) : kOOB);
       }
+      if (stage) {
+        const int qn = (nunits * 256 + 1023) / 1024;
+        for (int i = wave; i < kStageRows * qn; i += WK * WN) {
+          const int br = i / qn, q = i - (i / qn) * qn;
+          const int route = __builtin_amdgcn_readlane((int)my_route[0], br);
+          if (route < 0) continue;
+          const int64_t arow = (g.sorted_ids || g.route_ids) ? route / g.top_k : route;
+          const uint32_t kb = (uint32_t)(q * 1024 + lane * 16);
+          const uint32_t off = kb < (uint32_t)(g.k * (int)sizeof(T))
+                                   ? (uint32_t)(arow * g.lda * (int64_t)sizeof(T)) + kb
+                                   : kOOB;
+          llvm_amdgcn_raw_buffer_load_lds(rA, lds_ptr(a_lds + br * a_stride + q * 1024), 16, off,
+                                          0, 0, 0);
+        }
+      }
       V8 af[U][RB][4];
 #pragma unroll
       for (int uu = 0; uu < U; ++uu) {
@@ -178,9 +311,10 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
         const bool k_ok = k0 < g.k;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
+          const bool staged = stage && rb * 16 + c16 < kStageRows;
           // nothing in this branch consumes the loaded values, so no wait
           // is placed in it
-          if (k_ok && aoff[rb] != kOOB) {
+          if (k_ok && aoff[rb] != kOOB && !staged) {
             const uint32_t o = aoff[rb] + (uint32_t)(k0 * (int)sizeof(T));
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -190,6 +324,23 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
             for (int j = 0; j < 4; ++j) af[uu][rb][j] = zero_v8<V8>();
           }
         }
+      }
+      if (stage) {
+        // the staged rows have landed once every wave's loads are done
+        wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int uu = 0; uu < U; ++uu)
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) {
+            const int br = rb * 16 + c16;
+            const bool k_ok = (u0 + uu) * 128 + grp * 32 < g.k;
+            if (br < kStageRows && aoff[rb] != kOOB && k_ok) {
+              const uint8_t* src = a_lds + br * a_stride + (u0 + uu) * 256 + grp * 64;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) af[uu][rb][j] = *reinterpret_cast<const V8*>(src + 16 * j);
+            }
+          }
       }
 #pragma unroll
       for (int uu = 0; uu < U; ++uu) {
@@ -226,7 +377,9 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
     const int l = (idx >> 2) & 63;
     const int i = idx & 3;
     const int col = (blockIdx.x * WN * CG + cgi) * 16 + (l & 15);
-    const RowInfo r = row_info(g, pos0 + rb * 16 + (l >> 4) * 4 + i);
+    RowInfo r;
+    r.out_row = srow[rb * 16 + (l >> 4) * 4 + i];
+    r.valid = r.out_row >= 0;
     if (!r.valid || col >= g.n) continue;
     if (expert < 0) {
       static_cast<T*>(g.c)[r.out_row * g.ldc + col] = from_f32<T>(0.f);
@@ -479,11 +632,13 @@ SkinnyShape skinny_shape(int64_t k, int64_t n, int64_t row_blocks, int rb) {
 template <typename T, int RB, int CG, int EPI>
 void skinny_launch_cg(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStream_t st) {
   constexpr int U = RB == 1 ? 4 : 2;
+  const int nunits = (g.k + 127) / 128;
+  const size_t lds = nunits <= s.wk * U ? (size_t)kStageRows * stage_stride(nunits) : 0;
   switch (s.wk) {
-    case 1: w4a16_skinny<T, RB, 1, 4, CG, U, EPI><<<grid, 256, 0, st>>>(g); break;
-    case 2: w4a16_skinny<T, RB, 2, 2, CG, U, EPI><<<grid, 256, 0, st>>>(g); break;
-    case 4: w4a16_skinny<T, RB, 4, 1, CG, U, EPI><<<grid, 256, 0, st>>>(g); break;
-    default: w4a16_skinny<T, RB, 8, 1, CG, U, EPI><<<grid, 512, 0, st>>>(g); break;
+    case 1: w4a16_skinny<T, RB, 1, 4, CG, U, EPI><<<grid, 256, lds, st>>>(g); break;
+    case 2: w4a16_skinny<T, RB, 2, 2, CG, U, EPI><<<grid, 256, lds, st>>>(g); break;
+    case 4: w4a16_skinny<T, RB, 4, 1, CG, U, EPI><<<grid, 256, lds, st>>>(g); break;
+    default: w4a16_skinny<T, RB, 8, 1, CG, U, EPI><<<grid, 512, lds, st>>>(g); break;
   }
 }
 
@@ -501,7 +656,9 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
   // skinny for 16/32-row blocks (and any routed block size that is not a
   // multiple of 32); tiled otherwise.
   int skinny_rb = 0;
-  if (routed) {
+  if (g.route_ids) {
+    skinny_rb = 1;  // direct routing: one workgroup row per route
+  } else if (routed) {
     if (g.block_m % 32 != 0) skinny_rb = 1;
     else if (g.block_m == 32) skinny_rb = 2;
   } else if (cap <= 32) {
@@ -514,7 +671,7 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
   const int64_t lim = 0x7FFFFFFF;
   if (skinny_rb && (g.a_rows * g.lda * (int64_t)sizeof(T) > lim || b_rows_total * g.b_n > lim ||
                     b_rows_total * g.bs_n > lim)) {
-    if (routed && g.block_m % 32 != 0) {
+    if (g.route_ids || (routed && g.block_m % 32 != 0)) {
       set_error("w4a16: operands above 2 GiB need a routing block size that is a multiple of 32");
       return MXFP4_ERR_VALUE;
     }
@@ -522,15 +679,16 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
   }
   if (skinny_rb) {
     const int rb = skinny_rb;
-    const int64_t gy = (cap + 16 * rb - 1) / (16 * rb);
+    const int64_t gy = g.route_ids ? g.num_valid : (cap + 16 * rb - 1) / (16 * rb);
     if (gy > 65535) {
       set_error("w4a16: too many row blocks (%lld)", (long long)gy);
       return MXFP4_ERR_VALUE;
     }
     // active row blocks: dense rows, or at most one partial block per
     // routed expert plus the full ones
-    const int64_t blocks = routed ? std::min<int64_t>(gy, g.num_valid / (16 * rb) + g.num_experts)
-                                  : gy;
+    const int64_t blocks = (routed || g.route_ids)
+                               ? std::min<int64_t>(gy, g.num_valid / (16 * rb) + g.num_experts)
+                               : gy;
     const SkinnyShape sh = skinny_shape(g.k, out_cols, blocks, rb);
     const int tile_cols = 16 * sh.wn * sh.cg;
     dim3 grid((unsigned)((out_cols + tile_cols - 1) / tile_cols), (unsigned)(gy > 0 ? gy : 1));

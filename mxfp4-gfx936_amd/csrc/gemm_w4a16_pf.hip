@@ -34,23 +34,6 @@
 namespace mx {
 namespace {
 
-typedef __attribute__((address_space(3))) uint32_t lds_u32;
-
-extern "C" __device__ void llvm_amdgcn_raw_buffer_load_lds(i32x4 rsrc, lds_u32* lds, int size,
-                                                           int voffset, int soffset, int offset,
-                                                           int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.lds");
-
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ lds_u32* lds_ptr(uint8_t* p) {
-  return (lds_u32*)(__attribute__((address_space(3))) uint8_t*)p;
-}
-
 template <typename T>
 struct V8Of;
 template <>

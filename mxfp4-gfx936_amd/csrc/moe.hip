@@ -22,6 +22,10 @@ namespace mx {
 namespace {
 
 constexpr int kChunk = 1024;  // routes per count/place workgroup
+// Layers with at most this many routes use direct routing in the GEMMs
+// (no kernel builds sorted metadata); must not exceed the skinny kernel's
+// scan limit (256).
+constexpr int64_t kDirectRoutes = 64;
 constexpr int kMaxExperts = 1024;
 
 template <typename TI>
@@ -140,17 +144,122 @@ __global__ __launch_bounds__(256) void topk_sum(const T* __restrict__ d, const T
     const int64_t t = u / vecs;
     const int64_t c = (u - t * vecs) * 8;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < top_k; ++s) {
-      const int64_t e = (int64_t)ids[t * top_k + s];
-      if (e < 0 || e >= num_experts) continue;
-      const V8 v = *reinterpret_cast<const V8*>(d + (t * top_k + s) * hidden + c);
+    // eight slots per step, all loads issued before the first add (slots
+    // past top_k re-read the last one and are masked); the adds keep slot
+    // order
+    for (int s0 = 0; s0 < top_k; s0 += 8) {
+      V8 v[8];
+      bool ok[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += (float)v[j];
+      for (int q = 0; q < 8; ++q) {
+        const int s = s0 + q < top_k ? s0 + q : top_k - 1;
+        const int64_t e = (int64_t)ids[t * top_k + s];
+        ok[q] = (s0 + q < top_k) && e >= 0 && e < num_experts;
+        v[q] = *reinterpret_cast<const V8*>(d + (t * top_k + s) * hidden + c);
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (ok[q]) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j] += (float)v[q][j];
+        }
     }
     V8 o;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = from_f32<T>(acc[j]);
     *reinterpret_cast<V8*>(out + t * hidden + c) = o;
+  }
+}
+
+// All three passes in one workgroup for at most kChunk routes (decode and
+// small prefill): the histogram, the padded exclusive scan over experts
+// (each thread owns kMaxExperts / 256 consecutive experts), and the ballot
+// placement of align_place, separated by barriers instead of launches.
+template <typename TI>
+__global__ __launch_bounds__(256) void align_single(const TI* __restrict__ ids, int64_t n,
+                                                    int num_experts, int id_bits, int block_m,
+                                                    int32_t* __restrict__ sorted_ids,
+                                                    int32_t* __restrict__ expert_ids,
+                                                    int32_t* __restrict__ num_post_padded) {
+  constexpr int EPT = kMaxExperts / 256;  // experts per thread in the scan
+  __shared__ int cursor[kMaxExperts];     // counts, then start positions
+  __shared__ int wcnt[4][kMaxExperts];
+  __shared__ int part[256];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  for (int e = tid; e < kMaxExperts; e += 256) {
+    cursor[e] = 0;
+    wcnt[0][e] = wcnt[1][e] = wcnt[2][e] = wcnt[3][e] = 0;
+  }
+  __syncthreads();
+  int eid[kChunk / 256];
+#pragma unroll
+  for (int it = 0; it < kChunk / 256; ++it) {
+    const int64_t r = it * 256 + tid;
+    int64_t e64 = -1;
+    if (r < n) e64 = (int64_t)ids[r];
+    eid[it] = (e64 >= 0 && e64 < num_experts) ? (int)e64 : -1;
+    if (eid[it] >= 0) atomicAdd(&cursor[eid[it]], 1);
+  }
+  __syncthreads();
+  // padded exclusive scan: thread tid owns experts tid*EPT .. +EPT
+  int cnt[EPT], pad[EPT], local = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid * EPT + j;
+    cnt[j] = e < num_experts ? cursor[e] : 0;
+    pad[j] = (cnt[j] + block_m - 1) / block_m * block_m;
+    local += pad[j];
+  }
+  part[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int start = part[tid] - local;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid * EPT + j;
+    if (e < num_experts) {
+      cursor[e] = start;
+      for (int blk = start / block_m; blk < (start + pad[j]) / block_m; ++blk) expert_ids[blk] = e;
+      for (int p = start + cnt[j]; p < start + pad[j]; ++p) sorted_ids[p] = (int32_t)n;
+    }
+    start += pad[j];
+  }
+  if (tid == 255) num_post_padded[0] = part[255];
+  __syncthreads();
+  // placement in route order (align_place with this workgroup's cursors)
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int it = 0; it < kChunk / 256; ++it) {
+    const int64_t r = it * 256 + tid;
+    const bool valid = eid[it] >= 0;
+    const int e = valid ? eid[it] : 0;
+    uint64_t same = __ballot(valid);
+    for (int bit = 0; bit < id_bits; ++bit) {
+      const bool b = (e >> bit) & 1;
+      const uint64_t bal = __ballot(b);
+      same &= b ? bal : ~bal;
+    }
+    const int rank = __popcll(same & lt_mask);
+    if (valid && rank == 0) wcnt[wave][e] = __popcll(same);
+    __syncthreads();
+    if (valid) {
+      int before = cursor[e] + rank;
+      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
+      sorted_ids[before] = (int32_t)r;
+    }
+    __syncthreads();
+    for (int x = tid; x < num_experts; x += 256) {
+      cursor[x] += wcnt[0][x] + wcnt[1][x] + wcnt[2][x] + wcnt[3][x];
+      wcnt[0][x] = wcnt[1][x] = wcnt[2][x] = wcnt[3][x] = 0;
+    }
+    __syncthreads();
   }
 }
 
@@ -185,6 +294,11 @@ int launch_align(const TI* ids, int64_t n, int num_experts, int block_m, int32_t
                  hipStream_t st) {
   int id_bits = 0;
   while ((1 << id_bits) < num_experts) ++id_bits;
+  if (nchunks <= 1) {
+    align_single<TI><<<1, 256, 0, st>>>(ids, n, num_experts, id_bits, block_m, sorted_ids,
+                                        expert_ids, npp);
+    return launch_status("align launch");
+  }
   if (nchunks > 0) {
     align_count<TI><<<(unsigned)nchunks, 256, 0, st>>>(ids, n, num_experts, counts);
     int rc = launch_status("align count launch");
@@ -487,9 +601,14 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
   void* h = ws + p.off_h;
   void* d = ws + p.off_d;
 
-  rc = do_align(topk_ids, ids_dtype, p.routes, num_experts, p.block_m, sorted, experts, npp,
-                counts, p.nchunks, st);
-  if (rc) return rc;
+  // Few routes: the GEMMs find their rows from the top-k ids directly
+  // (direct routing), so no routing metadata is built.
+  const bool direct = p.routes <= kDirectRoutes && inter * hidden < ((int64_t)1 << 31);
+  if (!direct) {
+    rc = do_align(topk_ids, ids_dtype, p.routes, num_experts, p.block_m, sorted, experts, npp,
+                  counts, p.nchunks, st);
+    if (rc) return rc;
+  }
 
   // gate_up with the fused SiLU*mul epilogue: h[r, :inter]
   GemmArgs g = {};
@@ -515,8 +634,20 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
   g.block_m = p.block_m;
   g.inter = (int32_t)inter;
   g.num_experts = num_experts;
+  if (direct) {
+    g.sorted_ids = nullptr;
+    g.expert_ids = nullptr;
+    g.num_post_padded = nullptr;
+    g.route_ids = topk_ids;
+    g.ids64 = ids_dtype == MXFP4_DT_I64;
+  }
   rc = launch_w4a16(g, x_dtype, EPI_SILU_MUL, st);
   if (rc) return rc;
+  if (direct && top_k <= 16) {
+    // down with the route weight and the top-k sum in one kernel
+    return launch_moe_down_topk(h, w2, s2, topk_weights, topk_ids, ids_dtype == MXFP4_DT_I64, m,
+                                top_k, hidden, inter, num_experts, out, x_dtype, st);
+  }
 
   // down with the route weight: d[r, :hidden]
   GemmArgs g2 = g;
