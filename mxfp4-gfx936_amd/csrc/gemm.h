@@ -99,7 +99,12 @@ __device__ __forceinline__ float scalar_alpha(const GemmArgs& g, int expert) {
 // Host-side launchers (gemm_w4a16.hip, gemm_w4a4.hip).
 int launch_w4a16(const GemmArgs& g, int dtype, int epi, hipStream_t st);
 // Direct-to-LDS prefill kernel (gemm_w4a16_pf.hip): tile configurations.
-enum PfConfig { PF_128x256 = 0, PF_128x128 = 1, PF_64x128 = 2, PF_32x128 = 3 };
+enum PfConfig {
+  PF_128x256 = 0,  // 2 x 4 waves of 64 x 64
+  PF_128x128 = 1,  // 2 x 2 waves of 64 x 64
+  PF_64x128 = 2,   // 2 x 2 waves of 32 x 64, 3 stages
+  PF_32x128 = 3,   // 2 x 2 waves of 16 x 64, 3 stages
+};
 bool pf_supported(const GemmArgs& g, int elem_bytes);
 int pf_choose(const GemmArgs& g, int epi);
 int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t st);

@@ -1,7 +1,7 @@
 // W4A16 prefill GEMM, direct-to-LDS pipeline (gfx950).
 //
-// Tile BM x BN (output rows x weight rows), 256 threads = 2 x 2 waves, each
-// wave FM x FN MFMA blocks of 16x16, K in 64-deep stages:
+// Tile BM x BN (output rows x weight rows), WGM x WGN waves, each wave FM x
+// FN MFMA blocks of 16x16, K in 64-deep stages:
 //
 // * Staging.  A (BM x 64 bf16/fp16) and packed B (BN rows x 32 bytes) go
 //   global -> LDS with `buffer_load_dwordx4 ... lds` (16 bytes per lane land
@@ -18,7 +18,6 @@
 //   + the row's block scale) with four v_cvt_scalef32_pk_* right before the
 //   MFMA.  The MFMA takes the weights as its A operand and the activations as
 //   its B operand, so a lane owns 4 consecutive output columns of one row.
-//   A wave tile of 64 x 128 reads 192 LDS bytes per MFMA (vs 320 at 64 x 64).
 // * Epilogue.  Scales / route weight / bias / SiLU*mul are applied in
 //   registers, the tile is staged in LDS (reusing the stage buffers) and
 //   written back as full 16-byte chunks, whole output rows per instruction.
@@ -51,28 +50,41 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
 }
 
-template <int FM, int FN, int STAGES>
+template <int WGM, int WGN, int FM, int FN, int STAGES>
 struct PfShape {
-  static constexpr int BM = 2 * FM * 16;
-  static constexpr int BN = 2 * FN * 16;
+  static constexpr int NW = WGM * WGN;  // waves
+  static constexpr int NT = 64 * NW;    // threads
+  static constexpr int BM = WGM * FM * 16;
+  static constexpr int BN = WGN * FN * 16;
   static constexpr int A_STAGE = BM * 128;  // BM rows x 64 elements x 2 bytes
   static constexpr int B_STAGE = BN * 32;   // BN rows x 64 nibbles
-  static constexpr int S_SLOT = BN * 4;     // 4 scale bytes (128 K) per row
-  static constexpr int A_LOADS = BM / 32;   // 1 KB wave-loads per wave per stage
-  static constexpr int B_LOADS = BN / 128;
-  static constexpr int S_WAVES = BN / 64;   // waves that load a scale slot (64 rows each)
-  static constexpr int PIPE = STAGES * (A_STAGE + B_STAGE) + 2 * S_SLOT;
+  static constexpr int A_TOT = BM / 8;      // 1 KB wave-loads per stage (8 rows each)
+  static constexpr int B_TOT = BN / 32;     // (32 rows each)
+  static constexpr int S_TOT = (BN + 63) / 64;  // scale wave-loads (64 rows x 4 bytes)
+  static constexpr int A_PER = (A_TOT + NW - 1) / NW;
+  static constexpr int B_PER = (B_TOT + NW - 1) / NW;
+  static constexpr bool EVEN = A_TOT % NW == 0 && B_TOT % NW == 0;
+  static constexpr int S_SLOT = S_TOT * 256;  // 4 scale bytes (128 K) per row
+  // scale slots: one per stage pair, enough for every pair in flight
+  static constexpr int S_SLOTS = (STAGES + 2) / 2;
+  static constexpr int PIPE = STAGES * (A_STAGE + B_STAGE) + S_SLOTS * S_SLOT;
 };
 
-template <typename T, int FM, int FN, int STAGES, int EPI, int MINB>
-__global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int nbn) {
+template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB>
+__global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int nbm, int nbn) {
   typedef typename V8Of<T>::type V8;
-  typedef PfShape<FM, FN, STAGES> S;
-  constexpr int BM = S::BM, BN = S::BN;
+  typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
+  constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
   constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int C_LD = OUT_COLS * 2 + 16;  // bytes per staged output row
-  constexpr int SMEM = S::PIPE > BM * C_LD ? S::PIPE : BM * C_LD;
-  static_assert(S::S_WAVES <= 4 && BN % 128 == 0, "tile config");
+  // the finished tile is staged in LDS whole, or one wave row at a time
+  // when that would not fit in the pipeline buffers
+  constexpr int EPI_PASSES = BM * C_LD <= S::PIPE ? 1 : WGM;
+  constexpr int EPI_ROWS = BM / EPI_PASSES;
+  constexpr int SMEM = S::PIPE > EPI_ROWS * C_LD ? S::PIPE : EPI_ROWS * C_LD;
+  static_assert(S::S_TOT <= S::NW && BN % 32 == 0, "tile config");
+  static_assert(STAGES == 2 || S::EVEN, "multi-stage waits count loads per wave");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 stages");
   static_assert(EPI != EPI_SILU_MUL || FN % 2 == 0, "SiLU pairs need even FN");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
   uint8_t* const sA = smem;
@@ -82,7 +94,7 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int n
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int c16 = lane & 15;
   const int grp = lane >> 4;
 
@@ -104,7 +116,7 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int n
   const int ncol0 = bn * OUT_COLS;
 
   if (expert < 0) {  // aiter:156-172: expert not on this device -> zeros
-    for (int idx = tid; idx < BM * OUT_COLS; idx += 256) {
+    for (int idx = tid; idx < BM * OUT_COLS; idx += NT) {
       const int r = idx / OUT_COLS, cc = idx % OUT_COLS;
       const RowInfo ri = row_info(g, pos0 + r);
       if (ri.valid && ncol0 + cc < g.n)
@@ -122,6 +134,7 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int n
   // B-tile row -> weight row (or -1 past N).  With SiLU, 16-row blocks
   // alternate gate (even) and up (odd) rows of the same output columns.
   auto weight_row = [&](int i) -> int {
+    if (i >= BN) return -1;
     int orow, grow;
     if (EPI == EPI_SILU_MUL) {
       const int cbk = i >> 4;
@@ -134,25 +147,31 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int n
     return orow < g.n ? grow : -1;
   };
 
-  // ---- per-lane load offsets for stage 0; stage kt adds kt * stride
-  uint32_t a_off[S::A_LOADS];
+  // ---- per-lane load offsets for stage 0; stage kt adds kt * stride.
+  // Wave-load q of a stage (q < A_TOT / B_TOT) is issued by wave q % NW.
+  uint32_t a_off[S::A_PER];
 #pragma unroll
-  for (int j = 0; j < S::A_LOADS; ++j) {
-    const int row = (wave * S::A_LOADS + j) * 8 + (lane >> 3);
+  for (int j = 0; j < S::A_PER; ++j) {
+    const int q = j * S::NW + wave;
+    const int row = q * 8 + (lane >> 3);
     const int c = (lane & 7) ^ (row & 7);
-    const RowInfo ri = row_info(g, pos0 + row);
-    a_off[j] = ri.valid ? (uint32_t)(ri.a_row * g.lda * (int64_t)sizeof(T)) + c * 16 : kOOB;
+    a_off[j] = kOOB;
+    if (q < S::A_TOT) {
+      const RowInfo ri = row_info(g, pos0 + row);
+      if (ri.valid) a_off[j] = (uint32_t)(ri.a_row * g.lda * (int64_t)sizeof(T)) + c * 16;
+    }
   }
-  uint32_t b_off[S::B_LOADS];
+  uint32_t b_off[S::B_PER];
 #pragma unroll
-  for (int j = 0; j < S::B_LOADS; ++j) {
-    const int row = (wave * S::B_LOADS + j) * 32 + (lane >> 1);
+  for (int j = 0; j < S::B_PER; ++j) {
+    const int q = j * S::NW + wave;
+    const int row = q * 32 + (lane >> 1);
     const int c = (lane & 1) ^ ((row >> 3) & 1);
-    const int grow = weight_row(row);
+    const int grow = q < S::B_TOT ? weight_row(row) : -1;
     b_off[j] = grow >= 0 ? (uint32_t)(grow * g.b_n) + c * 16 : kOOB;
   }
   uint32_t s_off = kOOB;
-  if (wave < S::S_WAVES) {
+  if (wave < S::S_TOT) {
     const int grow = weight_row(wave * 64 + lane);
     s_off = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
   }
@@ -160,19 +179,23 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int n
   const int nk = g.k / 64;
   auto issue = [&](int kt) {
     const int st = kt % STAGES;
-    if ((kt & 1) == 0 && wave < S::S_WAVES)
-      llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + ((kt >> 1) & 1) * S::S_SLOT + wave * 256),
+    if ((kt & 1) == 0 && wave < S::S_TOT)
+      llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + wave * 256),
                                       4, (int)(s_off + (uint32_t)(kt >> 1) * 4u), 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < S::A_LOADS; ++j)
-      llvm_amdgcn_raw_buffer_load_lds(
-          rA, lds_ptr(sA + st * S::A_STAGE + (wave * S::A_LOADS + j) * 1024), 16,
-          (int)(a_off[j] + (uint32_t)kt * 128u), 0, 0, 0);
+    for (int j = 0; j < S::A_PER; ++j) {
+      const int q = j * S::NW + wave;
+      if (S::A_TOT % S::NW == 0 || q < S::A_TOT)
+        llvm_amdgcn_raw_buffer_load_lds(rA, lds_ptr(sA + st * S::A_STAGE + q * 1024), 16,
+                                        (int)(a_off[j] + (uint32_t)kt * 128u), 0, 0, 0);
+    }
 #pragma unroll
-    for (int j = 0; j < S::B_LOADS; ++j)
-      llvm_amdgcn_raw_buffer_load_lds(
-          rB, lds_ptr(sB + st * S::B_STAGE + (wave * S::B_LOADS + j) * 1024), 16,
-          (int)(b_off[j] + (uint32_t)kt * 32u), 0, 0, 0);
+    for (int j = 0; j < S::B_PER; ++j) {
+      const int q = j * S::NW + wave;
+      if (S::B_TOT % S::NW == 0 || q < S::B_TOT)
+        llvm_amdgcn_raw_buffer_load_lds(rB, lds_ptr(sB + st * S::B_STAGE + q * 1024), 16,
+                                        (int)(b_off[j] + (uint32_t)kt * 32u), 0, 0, 0);
+    }
   };
 
   // ---- per-lane LDS read offsets (fragment rows differ from c16 by
@@ -196,14 +219,18 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int n
     // outstanding.  A bare s_barrier (not __syncthreads, whose release fence
     // would drain every outstanding load) then publishes it to all waves and
     // retires the reads of the buffer the next issue() overwrites.
-    constexpr int PER_STAGE = S::A_LOADS + S::B_LOADS;
-    if (STAGES == 3 && kt + 1 < nk) wait_vmcnt<PER_STAGE>();
+    // (a wave's loads of one later stage number at most PER_STAGE, plus
+    // one scale load on even stages, which waiting for PER_STAGE covers)
+    constexpr int PER_STAGE = S::A_PER + S::B_PER;
+    const int later = (nk - 1 - kt) < (STAGES - 2) ? (nk - 1 - kt) : (STAGES - 2);
+    if (STAGES >= 4 && later >= 2) wait_vmcnt<2 * PER_STAGE>();
+    else if (STAGES >= 3 && later >= 1) wait_vmcnt<PER_STAGE>();
     else wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
     if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
     const uint8_t* As = sA + (kt % STAGES) * S::A_STAGE;
     const uint8_t* Bs = sB + (kt % STAGES) * S::B_STAGE;
-    const uint8_t* Ss = sS + ((kt >> 1) & 1) * S::S_SLOT + (kt & 1) * 2;
+    const uint8_t* Ss = sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       // logical chunk ks*4 + grp sits at physical chunk (grp ^ sw) ^ (ks*4):
@@ -224,74 +251,84 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pf(GemmArgs g, int nbm, int n
   }
 
   // ---- epilogue: lane owns row wm*FM*16 + fm*16 + c16 and columns
-  // fn*16 + grp*4 .. +3 of its wave's sub-tile; stage the finished tile in LDS
+  // fn*16 + grp*4 .. +3 of its wave's sub-tile; stage the finished rows in
+  // LDS and write whole 16-byte chunks
   __builtin_amdgcn_s_barrier();  // every wave is done reading the stage buffers
   const float alpha = scalar_alpha(g, expert);
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-    const int trow = wm * FM * 16 + fm * 16 + c16;
-    float rw = 1.0f;
-    if (g.route_w) {
+  for (int pass = 0; pass < EPI_PASSES; ++pass) {
+    if (EPI_PASSES == 1 || wm == pass) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int trow = wm * FM * 16 + fm * 16 + c16;
+        float rw = 1.0f;
+        if (g.route_w) {
+          const RowInfo r = row_info(g, pos0 + trow);
+          rw = r.valid ? g.route_w[r.out_row] : 0.f;
+        }
+        uint8_t* crow = smem + (trow - pass * EPI_ROWS) * C_LD;
+        if (EPI == EPI_SILU_MUL) {
+#pragma unroll
+          for (int fn = 0; fn < FN; fn += 2) {
+            const int tcol = ((wn * FN + fn) >> 1) * 16 + grp * 4;
+            float h[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              // vllm:249-252 on tensors of T: gate and up rounded to T, silu
+              // in FP32 rounded to T, the product rounded to T (below)
+              const T gb = from_f32<T>(acc[fm][fn][i] * alpha);
+              const T ub = from_f32<T>(acc[fm][fn + 1][i] * alpha);
+              const T sb = from_f32<T>(silu_f32(to_f32(gb)));
+              h[i] = to_f32(sb) * to_f32(ub);
+            }
+            *reinterpret_cast<uint2*>(crow + tcol * 2) =
+                uint2{pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
+          }
+        } else {
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) {
+            const int tcol = wn * FN * 16 + fn * 16 + grp * 4;
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = acc[fm][fn][i] * alpha * rw;
+            if (g.bias) {
+              const T* bp = static_cast<const T*>(g.bias) + ncol0 + tcol;
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (ncol0 + tcol + i < g.n) o[i] += to_f32(bp[i]);
+            }
+            *reinterpret_cast<uint2*>(crow + tcol * 2) =
+                uint2{pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3])};
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // whole 16-byte chunks, consecutive lanes along a row
+    constexpr int CHUNKS = OUT_COLS / 8;
+    for (int idx = tid; idx < EPI_ROWS * CHUNKS; idx += NT) {
+      const int prow = idx / CHUNKS, ch = idx % CHUNKS;
+      const int trow = pass * EPI_ROWS + prow;
+      const int col = ncol0 + ch * 8;
+      if (col >= g.n) continue;
       const RowInfo r = row_info(g, pos0 + trow);
-      rw = r.valid ? g.route_w[r.out_row] : 0.f;
-    }
-    uint8_t* crow = smem + trow * C_LD;
-    if (EPI == EPI_SILU_MUL) {
-#pragma unroll
-      for (int fn = 0; fn < FN; fn += 2) {
-        const int tcol = ((wn * FN + fn) >> 1) * 16 + grp * 4;
-        float h[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // vllm:249-252 on tensors of T: gate and up rounded to T, silu in
-          // FP32 rounded to T, the product rounded to T (below)
-          const T gb = from_f32<T>(acc[fm][fn][i] * alpha);
-          const T ub = from_f32<T>(acc[fm][fn + 1][i] * alpha);
-          const T sb = from_f32<T>(silu_f32(to_f32(gb)));
-          h[i] = to_f32(sb) * to_f32(ub);
-        }
-        *reinterpret_cast<uint2*>(crow + tcol * 2) = uint2{pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
-      }
-    } else {
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const int tcol = wn * FN * 16 + fn * 16 + grp * 4;
-        float o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = acc[fm][fn][i] * alpha * rw;
-        if (g.bias) {
-          const T* bp = static_cast<const T*>(g.bias) + ncol0 + tcol;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (ncol0 + tcol + i < g.n) o[i] += to_f32(bp[i]);
-        }
-        *reinterpret_cast<uint2*>(crow + tcol * 2) = uint2{pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3])};
+      if (!r.valid) continue;
+      const uint8_t* src = smem + prow * C_LD + ch * 16;
+      T* dst = static_cast<T*>(g.c) + r.out_row * g.ldc + col;
+      if (col + 8 <= g.n && (g.ldc & 7) == 0) {
+        *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
+      } else {
+        const T* s16 = reinterpret_cast<const T*>(src);
+        for (int i = 0; i < 8 && col + i < g.n; ++i) dst[i] = s16[i];
       }
     }
-  }
-  __syncthreads();
-  // whole 16-byte chunks, consecutive lanes along a row
-  constexpr int CHUNKS = OUT_COLS / 8;
-  for (int idx = tid; idx < BM * CHUNKS; idx += 256) {
-    const int trow = idx / CHUNKS, ch = idx % CHUNKS;
-    const int col = ncol0 + ch * 8;
-    if (col >= g.n) continue;
-    const RowInfo r = row_info(g, pos0 + trow);
-    if (!r.valid) continue;
-    const uint8_t* src = smem + trow * C_LD + ch * 16;
-    T* dst = static_cast<T*>(g.c) + r.out_row * g.ldc + col;
-    if (col + 8 <= g.n && (g.ldc & 7) == 0) {
-      *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
-    } else {
-      const T* s16 = reinterpret_cast<const T*>(src);
-      for (int i = 0; i < 8 && col + i < g.n; ++i) dst[i] = s16[i];
-    }
+    if (EPI_PASSES > 1 && pass + 1 < EPI_PASSES) __syncthreads();
   }
 }
 
-template <typename T, int FM, int FN, int STAGES, int EPI, int MINB>
+template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB>
 int launch_cfg(const GemmArgs& g, hipStream_t st) {
-  typedef PfShape<FM, FN, STAGES> S;
+  typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
   const int out_cols = (EPI == EPI_SILU_MUL) ? S::BN / 2 : S::BN;
   const int nbn = (g.n + out_cols - 1) / out_cols;
   const int64_t nbm = (g.m + S::BM - 1) / S::BM;
@@ -300,22 +337,27 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
     set_error("w4a16 prefill: bad grid");
     return MXFP4_ERR_VALUE;
   }
-  w4a16_pf<T, FM, FN, STAGES, EPI, MINB><<<(unsigned)nwg, 256, 0, st>>>(g, (int)nbm, nbn);
+  w4a16_pf<T, WGM, WGN, FM, FN, STAGES, EPI, MINB><<<(unsigned)nwg, S::NT, 0, st>>>(g, (int)nbm,
+                                                                                    nbn);
   return launch_status("w4a16 prefill launch");
 }
 
-// Tile configurations (BM x BN weight rows, stages, workgroups per CU).
-// Measured on MI355X (bf16): 128 x 128 / 2 stages is best for M = 4096 at
-// qkv (K 2048, N 5120) and o_proj (K 4096, N 2048) shapes, 128 x 256 once
-// there are >= 1024 such tiles (M 8192, K N 4096), 64 x 128 / 3 stages at
-// M ~ 370; smaller M uses 32 x 128.
+// Tile configurations (waves WGM x WGN, wave tile FM x FN MFMA blocks,
+// stages, workgroups per CU).  Measured on MI355X (bf16, medians of
+// interleaved runs): 128 x 128 with 4 waves and 2 stages is best at M 2048
+// - 4096 for qkv (K 2048, N 5120) and o_proj (K 4096, N 2048) shapes;
+// 128 x 256 with 8 waves wins by ~6% once there are >= 2048 128 x 128 tiles
+// (M 8192, K N 4096).  Rejected there: 4-wave 128 x 256 (64 x 128 per
+// wave), 256 x 160, 128 x 320, 256 x 256, 128 x 512, 192 x 256, and 3 or 4
+// stages (the extra LDS costs more occupancy than the deeper pipeline
+// gains).  64 x 128 / 3 stages suits M ~ 370; smaller M uses 32 x 128.
 template <typename T, int EPI>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
-    case PF_128x256: return launch_cfg<T, 4, 8, 2, EPI, 2>(g, st);
-    case PF_128x128: return launch_cfg<T, 4, 4, 2, EPI, 2>(g, st);
-    case PF_64x128: return launch_cfg<T, 2, 4, 3, EPI, 4>(g, st);
-    default: return launch_cfg<T, 1, 4, 3, EPI, 4>(g, st);
+    case PF_128x256: return launch_cfg<T, 2, 4, 4, 4, 2, EPI, 1>(g, st);
+    case PF_128x128: return launch_cfg<T, 2, 2, 4, 4, 2, EPI, 2>(g, st);
+    case PF_64x128: return launch_cfg<T, 2, 2, 2, 4, 3, EPI, 4>(g, st);
+    default: return launch_cfg<T, 2, 2, 1, 4, 3, EPI, 4>(g, st);
   }
 }
 
@@ -341,7 +383,7 @@ int pf_choose(const GemmArgs& g, int epi) {
     return ((g.m + bm - 1) / bm) * (int64_t)((g.n + out - 1) / out);
   };
   if (allowed(128)) {
-    if (tiles(128, 256) >= 1024) return PF_128x256;
+    if (tiles(128, 128) >= 2048) return PF_128x256;
     if (tiles(128, 128) >= 512) return PF_128x128;
   }
   if (allowed(64) && tiles(64, 128) >= 200) return PF_64x128;

@@ -114,6 +114,21 @@ def test_linear_attention_shapes(m, k, n):
     assert_parity(y[rows], oracle, ref=ref[rows], what=f"linear m={m} k={k} n={n}")
 
 
+@pytest.mark.parametrize("m,k,n", [(8192, 4096, 4096), (2100, 256, 16400)],
+                         ids=["cube", "partial_tiles"])
+def test_linear_wide_tile_shapes(m, k, n):
+    # >= 2048 tiles of 128 x 128 select the 8-wave 128 x 256 tile; the second
+    # shape ends in a partial row tile and a 16-column last tile
+    rng = np.random.default_rng(20261201 + m)
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    x = rand_act(20261201 + n, (m, k))
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    ref = _safe_reference(cuda(x), packed, scales)
+    rows = np.sort(np.concatenate([rng.choice(m, 96, replace=False), [m - 1]]))
+    oracle = O.linear_fp64(x.float().numpy()[rows], packed, scales)
+    assert_parity(y[rows], oracle, ref=ref[rows], what=f"linear m={m} k={k} n={n}")
+
+
 @pytest.mark.parametrize("m", [1, 20, 100])
 def test_linear_fp16_partial_tiles(m):
     rng = np.random.default_rng(m)
