@@ -9,8 +9,12 @@ N=5120 (bf16 activations ~N(0,1), E2M1 codes uniform 0..15, E8M0 scales
 uniform 120..128, seeded), in TFLOP/s.  A step is one
 ``linear_mxfp4_soft`` call on HBM-resident inputs; K steps are timed with a
 device synchronisation on both sides.  ``roofline`` is for that step's only
-kernel (w4a16_tiled), its average duration taken from HIP events on the
-stream it is launched on.  ``sweep`` carries the other BASELINE points:
+kernel (w4a16_pf, the direct-to-LDS prefill GEMM), its average duration
+taken from HIP events on the stream it is launched on; ``traffic`` is the
+HBM bytes per launch measured with rocprofv3 counters (FETCH_SIZE and
+WRITE_SIZE, each scaled by what the counter reads for a copy of known size)
+on ``bench.py --traffic-probe`` and recorded in
+profiles/w4a16_pf_qkv_prefill_traffic.md, or null when that file is absent.  ``sweep`` carries the other BASELINE points:
 decode W4A16 GEMV (HBM GB/s, weights rotated over >= 512 MB so the 256 MB
 MALL cannot serve them, launches replayed from a HIP graph), the routed MoE
 layer (us), W4A4 on the block-scaled FP4 MFMA, and the standalone dequant.
@@ -102,6 +106,57 @@ def time_graph(fns, replays=20):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / (replays * len(fns))
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w4a16_pf_qkv_prefill_traffic.md")
+COPY_BYTES = 256 << 20  # the calibration copy of --traffic-probe, each direction
+
+
+def recorded_traffic():
+    """HBM bytes per headline launch from the committed counter summary:
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the prefill kernel, each
+    scaled by COPY_BYTES / (the counter's reading for the calibration copy)."""
+    vals = {}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("- ") and ":" in line:
+                    key, _, val = line[2:].partition(":")
+                    try:
+                        vals[key.strip()] = float(val.split()[0])
+                    except (ValueError, IndexError):
+                        pass
+    except OSError:
+        return None
+    need = ("kernel_fetch_kib", "kernel_write_kib", "copy_fetch_kib", "copy_write_kib")
+    if not all(k in vals and vals[k] > 0 for k in need):
+        return None
+    fetch = vals["kernel_fetch_kib"] * COPY_BYTES / vals["copy_fetch_kib"]
+    write = vals["kernel_write_kib"] * COPY_BYTES / vals["copy_write_kib"]
+    return int(round(fetch + write))
+
+
+def traffic_probe() -> int:
+    """Headline kernel launches plus a 256 MiB device copy, for counter runs
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE -- python3 bench.py --traffic-probe)."""
+    import numpy as np
+    import torch
+
+    import mxfp4_amd as mx
+    mx._lib.load()
+    m, k, n = 4096, 2048, 5120
+    rng = np.random.default_rng(20260810 + 1)
+    (w, s), = rand_weights(rng, (n,), k)
+    x = randn_bf16(20260810, (m, k))
+    for _ in range(12):
+        mx.linear_mxfp4_soft(x, w, s)
+    a = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "traffic", "linear_launches": 12, "copy_bytes": COPY_BYTES}))
+    return 0
 
 
 def linear_bytes(m, n, k):
@@ -241,11 +296,16 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the launches the counter runs measure")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         return 2
+
+    if args.traffic_probe:
+        return traffic_probe()
 
     import numpy as np
     import torch
@@ -295,7 +355,8 @@ def main() -> int:
                    "activations": "bf16"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "w4a16_pf<bf16> 128x128 tile (direct-to-LDS)",
+                     "traffic": recorded_traffic(),
+                     "kernel": "w4a16_pf<bf16> 128x128 tile (direct-to-LDS)",
                      "kernel_us": round(kernel_ms * 1e3, 3),
                      "algorithmic_bytes": linear_bytes(m, n, k)},
     }
