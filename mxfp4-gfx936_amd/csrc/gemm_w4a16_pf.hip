@@ -98,17 +98,29 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   const int c16 = lane & 15;
   const int grp = lane >> 4;
 
-  // ---- tile order: XCD-contiguous ranges, groups of 4 row blocks
-  int pid = blockIdx.x;
-  {
+  // ---- tile order.  Workgroup i runs on XCD i % 8.  Dense: each XCD gets a
+  // contiguous range of tiles, walked in groups of 4 row blocks, keeping
+  // its A rows and B columns L2-resident.  Routed: the grid covers the
+  // capacity of sorted_ids and only the first num_post_padded rows are
+  // live, so contiguous ranges would leave the XCDs holding the tail idle;
+  // instead row blocks are dealt round-robin over the XCDs (the host pads
+  // the row-block count to a multiple of 8), each XCD walking all column
+  // tiles of one row block (one expert's weights, shared A rows) at a time.
+  int bm, bn;
+  if (g.sorted_ids) {
+    const int x = blockIdx.x % 8, i = blockIdx.x / 8;
+    bm = x + 8 * (i / nbn);
+    bn = i % nbn;
+  } else {
+    int pid = blockIdx.x;
     const int nwg = gridDim.x, per = nwg / 8, rem = nwg % 8, x = pid % 8, i = pid / 8;
     pid = x * per + (x < rem ? x : rem) + i;
+    constexpr int GROUP = 4;
+    const int first_m = (pid / (GROUP * nbn)) * GROUP;
+    const int gsize = (nbm - first_m) < GROUP ? (nbm - first_m) : GROUP;
+    bm = first_m + (pid % (GROUP * nbn)) % gsize;
+    bn = (pid % (GROUP * nbn)) / gsize;
   }
-  constexpr int GROUP = 4;
-  const int first_m = (pid / (GROUP * nbn)) * GROUP;
-  const int gsize = (nbm - first_m) < GROUP ? (nbm - first_m) : GROUP;
-  const int bm = first_m + (pid % (GROUP * nbn)) % gsize;
-  const int bn = (pid % (GROUP * nbn)) / gsize;
 
   const int64_t pos0 = (int64_t)bm * BM;
   if (pos0 >= rows_in_use(g)) return;
@@ -147,7 +159,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     return orow < g.n ? grow : -1;
   };
 
-  // ---- per-lane load offsets for stage 0; stage kt adds kt * stride.
+  // ---- per-lane load offsets for stage 0; stage kt adds kt * stride as
+  // the instruction's scalar offset (no per-stage vector adds; offsets of
+  // padding lanes stay past the end of the buffer).
   // Wave-load q of a stage (q < A_TOT / B_TOT) is issued by wave q % NW.
   uint32_t a_off[S::A_PER];
 #pragma unroll
@@ -181,20 +195,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     const int st = kt % STAGES;
     if ((kt & 1) == 0 && wave < S::S_TOT)
       llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + wave * 256),
-                                      4, (int)(s_off + (uint32_t)(kt >> 1) * 4u), 0, 0, 0);
+                                      4, (int)s_off, (kt >> 1) * 4, 0, 0);
 #pragma unroll
     for (int j = 0; j < S::A_PER; ++j) {
       const int q = j * S::NW + wave;
       if (S::A_TOT % S::NW == 0 || q < S::A_TOT)
         llvm_amdgcn_raw_buffer_load_lds(rA, lds_ptr(sA + st * S::A_STAGE + q * 1024), 16,
-                                        (int)(a_off[j] + (uint32_t)kt * 128u), 0, 0, 0);
+                                        (int)a_off[j], kt * 128, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < S::B_PER; ++j) {
       const int q = j * S::NW + wave;
       if (S::B_TOT % S::NW == 0 || q < S::B_TOT)
         llvm_amdgcn_raw_buffer_load_lds(rB, lds_ptr(sB + st * S::B_STAGE + q * 1024), 16,
-                                        (int)(b_off[j] + (uint32_t)kt * 32u), 0, 0, 0);
+                                        (int)b_off[j], kt * 32, 0, 0);
     }
   };
 
@@ -331,7 +345,8 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
   typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
   const int out_cols = (EPI == EPI_SILU_MUL) ? S::BN / 2 : S::BN;
   const int nbn = (g.n + out_cols - 1) / out_cols;
-  const int64_t nbm = (g.m + S::BM - 1) / S::BM;
+  int64_t nbm = (g.m + S::BM - 1) / S::BM;
+  if (g.sorted_ids) nbm = (nbm + 7) / 8 * 8;  // row blocks dealt over 8 XCDs
   const int64_t nwg = nbm * nbn;
   if (nwg <= 0 || nwg > 0x7FFFFFFF) {
     set_error("w4a16 prefill: bad grid");
@@ -343,21 +358,24 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 }
 
 // Tile configurations (waves WGM x WGN, wave tile FM x FN MFMA blocks,
-// stages, workgroups per CU).  Measured on MI355X (bf16, medians of
-// interleaved runs): 128 x 128 with 4 waves and 2 stages is best at M 2048
-// - 4096 for qkv (K 2048, N 5120) and o_proj (K 4096, N 2048) shapes;
-// 128 x 256 with 8 waves wins by ~6% once there are >= 2048 128 x 128 tiles
-// (M 8192, K N 4096).  Rejected there: 4-wave 128 x 256 (64 x 128 per
-// wave), 256 x 160, 128 x 320, 256 x 256, 128 x 512, 192 x 256, and 3 or 4
-// stages (the extra LDS costs more occupancy than the deeper pipeline
-// gains).  64 x 128 / 3 stages suits M ~ 370; smaller M uses 32 x 128.
+// stages, workgroups per CU).  Every configuration puts its waves side by
+// side on columns (WGM = 1): a wave then spans all BM rows, so each decoded
+// weight fragment feeds BM / 16 MFMAs and the per-MFMA decode work is the
+// smallest the tile allows (measured +2-7% at 128 rows, +13-15% at 32-64
+// rows against 2 x 2 waves).  Medians of interleaved MI355X runs (bf16):
+// 128 x 128 for M = 4096 at qkv / o_proj shapes, 128 x 256 (8 waves) once
+// there are >= 2048 128 x 128 tiles (M 8192 K N 4096: +5%), 64 x 128 and
+// 32 x 128 (3 stages) for mid M (M ~ 1024 and ~ 370, and MoE blocks of 64).
+// Rejected: 256 x 160, 128 x 320, 256 x 256, 128 x 512, 192 x 256, 64 x
+// 256/512, 32 x 256/512, and 3-4 stages at 128 rows (the extra LDS costs more
+// occupancy than the deeper pipeline gains).
 template <typename T, int EPI>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
-    case PF_128x256: return launch_cfg<T, 2, 4, 4, 4, 2, EPI, 1>(g, st);
-    case PF_128x128: return launch_cfg<T, 2, 2, 4, 4, 2, EPI, 2>(g, st);
-    case PF_64x128: return launch_cfg<T, 2, 2, 2, 4, 3, EPI, 4>(g, st);
-    default: return launch_cfg<T, 2, 2, 1, 4, 3, EPI, 4>(g, st);
+    case PF_128x256: return launch_cfg<T, 1, 8, 8, 2, 2, EPI, 1>(g, st);
+    case PF_128x128: return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2>(g, st);
+    case PF_64x128: return launch_cfg<T, 1, 4, 4, 2, 3, EPI, 4>(g, st);
+    default: return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4>(g, st);
   }
 }
 
@@ -386,7 +404,7 @@ int pf_choose(const GemmArgs& g, int epi) {
     if (tiles(128, 128) >= 2048) return PF_128x256;
     if (tiles(128, 128) >= 512) return PF_128x128;
   }
-  if (allowed(64) && tiles(64, 128) >= 200) return PF_64x128;
+  if (allowed(64) && tiles(64, 128) >= 512) return PF_64x128;
   return PF_32x128;
 }
 
