@@ -109,6 +109,15 @@ bool pf_supported(const GemmArgs& g, int elem_bytes);
 int pf_choose(const GemmArgs& g, int epi);
 int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t st);
 int launch_w4a4(const GemmArgs& g, int out_dtype, hipStream_t st);
+// Direct-to-LDS W4A4 kernel (gemm_w4a4_pf.hip).
+enum P4Config {
+  P4_256x256 = 0,  // 2 x 4 waves of 128 x 64, 3 stages
+  P4_128x128 = 1,  // 1 x 4 waves of 128 x 32
+  P4_64x128 = 2,   // 1 x 4 waves of 64 x 32
+};
+bool p4_supported(const GemmArgs& g);
+int p4_choose(const GemmArgs& g, int out_dtype);  // -1: not applicable
+int launch_w4a4_pf(const GemmArgs& g, int out_dtype, int cfg, hipStream_t st);
 int launch_f32_reference(const GemmArgs& g, int a_dtype, hipStream_t st);
 // MoE decode: down projection fused with the top-k combine (moe_decode.hip);
 // h holds the m * top_k routes' rows of width inter in route order.

@@ -220,6 +220,10 @@ int launch_w4a4_typed(const GemmArgs& g, hipStream_t st) {
 }  // namespace
 
 int launch_w4a4(const GemmArgs& g, int out_dtype, hipStream_t st) {
+  if (out_dtype == MXFP4_DT_BF16 || out_dtype == MXFP4_DT_F16 || out_dtype == MXFP4_DT_F32) {
+    const int cfg = p4_supported(g) ? p4_choose(g, out_dtype) : -1;
+    if (cfg >= 0) return launch_w4a4_pf(g, out_dtype, cfg, st);
+  }
   switch (out_dtype) {
     case MXFP4_DT_BF16: return launch_w4a4_typed<__bf16>(g, st);
     case MXFP4_DT_F16: return launch_w4a4_typed<_Float16>(g, st);

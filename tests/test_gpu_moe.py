@@ -157,6 +157,30 @@ def test_aiter_entry_uses_metadata(block_m):
     assert_parity(out, oracle)
 
 
+@pytest.mark.parametrize("block_m", [64, 128, 256])
+def test_aiter_entry_w4a4_metadata(block_m):
+    # packed MXFP4 activations through caller metadata, with an expert -1
+    # block and enough routes to fill several row blocks per expert
+    rng = np.random.default_rng(block_m + 1)
+    m, k, n, e, top_k = 300, 256, 320, 4, 2
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    ap, asc = O.quant_mxfp4_ties_away(rand_act(block_m + 7, (m, k)).float().numpy())
+    w, ids = _route(m, e, top_k, 200 + block_m)
+    srt, exp_, npp = O.make_routing(ids.numpy(), block_m=block_m, num_experts=e)
+    exp_ = exp_.copy()
+    exp_[exp_ == 1] = -1
+    C = torch.full((m, top_k, n), 3.0, dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4(cuda(ap), cuda(wp), C, torch.tensor([0.5], device="cuda"),
+                       torch.linspace(1, 2, e, device="cuda"), cuda(asc), cuda(ws), cuda(w),
+                       cuda(ids), cuda(srt), cuda(exp_), cuda(npp), True, top_k, False, False,
+                       {"BLOCK_SIZE_M": block_m}, torch.bfloat16)
+    ids_np = ids.numpy()
+    oracle = O.fused_moe_fp64(O.dequant_values(ap, asc, "bf16"), wp, ws, 0.5,
+                              np.linspace(1, 2, e), w.numpy(), ids_np, True)
+    oracle[ids_np == 1] = 0.0
+    assert_parity(C.float().cpu().numpy(), oracle)
+
+
 # ---------------------------------------------------------------- routing
 
 @pytest.mark.parametrize("n_tokens,top_k,num_experts,block_m",

@@ -59,6 +59,24 @@ def test_w4a4_linear(m, k, n, out_dtype):
     del rng
 
 
+@pytest.mark.parametrize("m,n,out_dtype", [(2048, 4096, torch.bfloat16), (2048, 2048, torch.float16),
+                                           (2048, 4096, torch.float32), (1000, 4100, torch.bfloat16)],
+                         ids=["128x256", "128x128", "f32_out", "partial"])
+def test_w4a4_tile_configs(m, n, out_dtype):
+    # grids large enough for the 128 x 256 / 128 x 128 tiles, FP32 output,
+    # and partial row / column tiles; checked on sampled rows
+    k = 256
+    a = rand_act(m + 1, (m, k)).float().numpy()
+    w = (rand_act(n + 2, (n, k)).float() * 0.02).numpy()
+    ap, asc = O.quant_mxfp4_rne(a)
+    wp, wsc = O.quant_mxfp4_rne(w)
+    y = mx.linear_mxfp4_w4a4(cuda(ap), cuda(asc), cuda(wp), cuda(wsc), out_dtype)
+    assert y.dtype == out_dtype and y.shape == (m, n)
+    rows = np.sort(np.concatenate([np.random.default_rng(m).choice(m, 48, replace=False), [m - 1]]))
+    oracle = O.dequant_values(ap[rows], asc[rows], "f32") @ O.dequant_values(wp, wsc, "f32").T
+    assert_parity(y[torch.from_numpy(rows).cuda()], oracle, what=f"w4a4 {m}x{k}x{n}")
+
+
 def test_w4a4_baseline_shape_sampled():
     # M=8192, K=4096, N=4096 (checked on sampled rows)
     m, k, n = 8192, 4096, 4096
