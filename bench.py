@@ -159,6 +159,50 @@ def traffic_probe() -> int:
     return 0
 
 
+def decode_probe() -> int:
+    """Decode launches for counter and trace runs of the bandwidth-bound
+    kernels: dense W4A16 GEMV (qkv M=1 and 8, o_proj M=1) over rotated weight
+    copies (>= 256 MB, so the MALL cannot hold them), the MoE layer at M=1
+    and 8 over 2 weight copies, then the 256 MiB calibration copy."""
+    import numpy as np
+    import torch
+
+    import mxfp4_amd as mx
+    mx._lib.load()
+    for name, k, n, ms in (("qkv", 2048, 5120, (1, 8)), ("o_proj", 4096, 2048, (1,))):
+        rng = np.random.default_rng(20260811 + k)
+        copies = (300 << 20) // (n * k // 2 + n * k // 32) + 1
+        ws = rand_weights(rng, (n,), k, copies)
+        for m in ms:
+            x = randn_bf16(20260811 + m, (m, k))
+            for p, s in ws:
+                mx.linear_mxfp4_soft(x, p, s)
+        del ws
+    e, hidden, inter, top_k = 128, 2048, 768, 8
+    rng = np.random.default_rng(20260815)
+    layers = []
+    for _ in range(2):
+        (w13, s13), = rand_weights(rng, (e, 2 * inter), hidden)
+        (w2, s2), = rand_weights(rng, (e, hidden), inter)
+        layers.append((w13, s13, w2, s2))
+    for m in (1, 8):
+        g = torch.Generator().manual_seed(20260817 + m)
+        w, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
+        w = (w / w.sum(-1, keepdim=True)).cuda()
+        ids = ids.cuda()
+        x = randn_bf16(20260816 + m, (m, hidden))
+        for _ in range(3):
+            for c in layers:
+                mx.moe_layer(x, *c, w, ids)
+    a = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "decode", "copy_bytes": COPY_BYTES}))
+    return 0
+
+
 def linear_bytes(m, n, k):
     return n * k // 2 + n * k // 32 + 2 * m * k + 2 * m * n
 
@@ -298,6 +342,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the launches the counter runs measure")
+    ap.add_argument("--decode-probe", action="store_true",
+                    help="only run decode launches for counter / trace runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -306,6 +352,8 @@ def main() -> int:
 
     if args.traffic_probe:
         return traffic_probe()
+    if args.decode_probe:
+        return decode_probe()
 
     import numpy as np
     import torch
