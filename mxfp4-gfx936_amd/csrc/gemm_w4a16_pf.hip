@@ -367,8 +367,9 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 // there are >= 2048 128 x 128 tiles (M 8192 K N 4096: +5%), 64 x 128 and
 // 32 x 128 (3 stages) for mid M (M ~ 1024 and ~ 370, and MoE blocks of 64).
 // Rejected: 256 x 160, 128 x 320, 256 x 256, 128 x 512, 192 x 256, 64 x
-// 256/512, 32 x 256/512, wave tiles of 128 x 64 (2 or 4 waves), and 3-4
-// stages at 128 rows (the extra LDS or registers cost more occupancy than
+// 256/512, 32 x 256/512, wave tiles of 128 x 64 (2 or 4 waves), 128 x
+// 160 / 128 x 320 (5 / 10 waves: a wave count that is not a multiple of
+// the 4 SIMDs loads one SIMD twice), and 3-4 stages at 128 rows (the extra LDS or registers cost more occupancy than
 // the deeper pipeline or the fewer LDS reads gain).
 template <typename T, int EPI>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {

@@ -22,6 +22,7 @@ namespace mx {
 namespace {
 
 constexpr int kChunk = 1024;  // routes per count/place workgroup
+constexpr int kSingle = 4096;  // routes the single-workgroup routing handles
 // Layers with at most this many routes use direct routing in the GEMMs
 // (no kernel builds sorted metadata); must not exceed the skinny kernel's
 // scan limit (256).
@@ -55,13 +56,21 @@ __global__ __launch_bounds__(1024) void align_scan(int32_t* __restrict__ counts,
                                                    int32_t* __restrict__ num_post_padded) {
   __shared__ int scan[kMaxExperts];
   const int e = threadIdx.x;
+  // exclusive prefix over chunks within the expert, eight chunks' counts
+  // loaded before any is rewritten (one memory round trip per 8 chunks)
   int total = 0;
   if (e < num_experts) {
-    for (int b = 0; b < nchunks; ++b) {
-      const int64_t idx = (int64_t)b * num_experts + e;
-      const int c = counts[idx];
-      counts[idx] = total;  // exclusive prefix within the expert
-      total += c;
+    for (int b0 = 0; b0 < nchunks; b0 += 8) {
+      int c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        c[j] = b0 + j < nchunks ? counts[(int64_t)(b0 + j) * num_experts + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (b0 + j < nchunks) {
+          counts[(int64_t)(b0 + j) * num_experts + e] = total;
+          total += c[j];
+        }
     }
   }
   const int padded = ((total + block_m - 1) / block_m) * block_m;
@@ -76,7 +85,15 @@ __global__ __launch_bounds__(1024) void align_scan(int32_t* __restrict__ counts,
   }
   const int start = scan[e] - padded;  // exclusive
   if (e < num_experts) {
-    for (int b = 0; b < nchunks; ++b) counts[(int64_t)b * num_experts + e] += start;
+    for (int b0 = 0; b0 < nchunks; b0 += 8) {
+      int c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        c[j] = b0 + j < nchunks ? counts[(int64_t)(b0 + j) * num_experts + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (b0 + j < nchunks) counts[(int64_t)(b0 + j) * num_experts + e] = c[j] + start;
+    }
     for (int blk = start / block_m; blk < (start + padded) / block_m; ++blk) expert_ids[blk] = e;
     for (int p = start + total; p < start + padded; ++p) sorted_ids[p] = (int32_t)n;
   }
@@ -171,7 +188,7 @@ __global__ __launch_bounds__(256) void topk_sum(const T* __restrict__ d, const T
   }
 }
 
-// All three passes in one workgroup for at most kChunk routes (decode and
+// All three passes in one workgroup for at most kSingle routes (decode and
 // small prefill): the histogram, the padded exclusive scan over experts
 // (each thread owns kMaxExperts / 256 consecutive experts), and the ballot
 // placement of align_place, separated by barriers instead of launches.
@@ -193,9 +210,9 @@ __global__ __launch_bounds__(256) void align_single(const TI* __restrict__ ids, 
     wcnt[0][e] = wcnt[1][e] = wcnt[2][e] = wcnt[3][e] = 0;
   }
   __syncthreads();
-  int eid[kChunk / 256];
+  int eid[kSingle / 256];
 #pragma unroll
-  for (int it = 0; it < kChunk / 256; ++it) {
+  for (int it = 0; it < kSingle / 256; ++it) {
     const int64_t r = it * 256 + tid;
     int64_t e64 = -1;
     if (r < n) e64 = (int64_t)ids[r];
@@ -236,7 +253,7 @@ __global__ __launch_bounds__(256) void align_single(const TI* __restrict__ ids, 
   // placement in route order (align_place with this workgroup's cursors)
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
-  for (int it = 0; it < kChunk / 256; ++it) {
+  for (int it = 0; it < kSingle / 256; ++it) {
     const int64_t r = it * 256 + tid;
     const bool valid = eid[it] >= 0;
     const int e = valid ? eid[it] : 0;
@@ -294,7 +311,7 @@ int launch_align(const TI* ids, int64_t n, int num_experts, int block_m, int32_t
                  hipStream_t st) {
   int id_bits = 0;
   while ((1 << id_bits) < num_experts) ++id_bits;
-  if (nchunks <= 1) {
+  if (n <= kSingle) {
     align_single<TI><<<1, 256, 0, st>>>(ids, n, num_experts, id_bits, block_m, sorted_ids,
                                         expert_ids, npp);
     return launch_status("align launch");
