@@ -22,7 +22,10 @@ namespace mx {
 namespace {
 
 constexpr int kChunk = 1024;  // routes per count/place workgroup
-constexpr int kSingle = 4096;  // routes the single-workgroup routing handles
+// Routes the single-workgroup routing handles: at 1024 it replaces three
+// launches with one 7 us kernel; at 4096 its serial 256-route passes took
+// 24 us against 16 us for the three-launch path.
+constexpr int kSingle = 1024;
 // Layers with at most this many routes use direct routing in the GEMMs
 // (no kernel builds sorted metadata); must not exceed the skinny kernel's
 // scan limit (256).
