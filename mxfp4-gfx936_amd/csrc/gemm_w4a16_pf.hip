@@ -245,22 +245,35 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     const uint8_t* As = sA + (kt % STAGES) * S::A_STAGE;
     const uint8_t* Bs = sB + (kt % STAGES) * S::B_STAGE;
     const uint8_t* Ss = sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2;
+    // All LDS reads of the stage first (the reads of ks = 1 overlap the
+    // MFMAs of ks = 0), then per ks: decode every weight fragment, then the
+    // FM x FN MFMAs back to back.  Logical chunk ks*4 + grp of an A row sits
+    // at physical chunk (grp ^ sw) ^ (ks*4): flipping bit 6 of the byte
+    // offset selects the ks = 1 half.
+    V8 af[2][FM];
+    uint32_t raw[2][FN];
+    uint32_t sb[2][FN];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      // logical chunk ks*4 + grp sits at physical chunk (grp ^ sw) ^ (ks*4):
-      // flipping bit 6 of the byte offset selects the ks = 1 half
-      V8 af[FM];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
-        af[fm] = *reinterpret_cast<const V8*>(As + ((a_rd0 + fm * 16 * 128) ^ (ks * 64)));
+        af[ks][fm] = *reinterpret_cast<const V8*>(As + ((a_rd0 + fm * 16 * 128) ^ (ks * 64)));
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) {
-        const uint32_t raw =
+        raw[ks][fn] =
             *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 16 * 32 + ((ks ^ b_sw) * 16));
-        const V8 bf = Decode<T>::run(raw, e8m0_scale(Ss[s_rd + fn * 16 * 4 + ks]));
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) acc[fm][fn] = mfma16(bf, af[fm], acc[fm][fn]);
+        sb[ks][fn] = Ss[s_rd + fn * 16 * 4 + ks];
       }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      V8 bf[FN];
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) bf[fn] = Decode<T>::run(raw[ks][fn], e8m0_scale(sb[ks][fn]));
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) acc[fm][fn] = mfma16(bf[fn], af[ks][fm], acc[fm][fn]);
     }
   }
 
