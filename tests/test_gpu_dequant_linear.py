@@ -129,6 +129,22 @@ def test_linear_wide_tile_shapes(m, k, n):
     assert_parity(y[rows], oracle, ref=ref[rows], what=f"linear m={m} k={k} n={n}")
 
 
+def test_linear_rejects_k_not_multiple_of_128():
+    # soft:326-327: the module and the C ABI both refuse K % 128 != 0
+    rng = np.random.default_rng(700)
+    n, k, m = 64, 2080, 4
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    x = rand_act(700, (m, k))
+    with pytest.raises(ValueError):
+        mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    xd, wd, sd = cuda(x), cuda(packed), cuda(scales)
+    y = torch.empty((m, n), dtype=x.dtype, device="cuda")
+    lib = _lib.load()
+    rc = lib.mxfp4_linear_w4a16(_lib.ptr(xd), _lib.dtype_code(x.dtype), m, k, k, _lib.ptr(wd),
+                                _lib.ptr(sd), n, None, _lib.ptr(y), _lib.stream_of(xd.device))
+    assert rc == _lib.ERR_VALUE
+
+
 @pytest.mark.parametrize("m", [1, 20, 100])
 def test_linear_fp16_partial_tiles(m):
     rng = np.random.default_rng(m)

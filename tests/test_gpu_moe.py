@@ -231,6 +231,24 @@ def test_moe_layer_vs_oracle(m, layer_weights):
     assert_layer_parity(y[t(rows).cuda()], oracle, safe, what=f"moe layer m={m}")
 
 
+def test_moe_layer_hidden_not_multiple_of_128():
+    # hidden 1056 (K % 128 == 32 for gate_up): routed blocks of 64 go to the
+    # register-staged tiled kernel; inter 320 keeps the down GEMM on it too
+    rng = np.random.default_rng(1056)
+    e, hidden, inter, top_k, m = 8, 1056, 320, 2, 256
+    w13, s13 = rand_mxfp4(rng, (e, 2 * inter), hidden)
+    w2, s2 = rand_mxfp4(rng, (e, hidden), inter)
+    x = rand_act(1056, (m, hidden))
+    w, ids = _route(m, e, top_k, 1057)
+    y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
+    rows = np.sort(np.random.default_rng(3).choice(m, 24, False))
+    oracle = O.moe_layer_fp64(x.float().numpy()[rows], w13, s13, w2, s2, w.numpy()[rows],
+                              ids.numpy()[rows])
+    t = torch.from_numpy
+    safe = O.moe_layer_safe(x[rows], t(w13), t(s13), t(w2), t(s2), w[rows], ids[rows])
+    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="moe layer hidden 1056")
+
+
 def test_moe_layer_small_vs_golden_and_safe():
     import os
     g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
