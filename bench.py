@@ -8,7 +8,10 @@ prefill point: the dense W4A16 linear at qkv_proj shape M=4096, K=2048,
 N=5120 (bf16 activations ~N(0,1), E2M1 codes uniform 0..15, E8M0 scales
 uniform 120..128, seeded), in TFLOP/s.  A step is one
 ``linear_mxfp4_soft`` call on HBM-resident inputs; K steps are timed with a
-device synchronisation on both sides.  ``roofline`` is for that step's only
+device synchronisation on both sides, after W untimed warmup steps that
+follow an untimed clock ramp (RAMP_MS of back-to-back calls: MI355X takes
+~10-15 ms of sustained work to reach its steady clocks, and every timing
+here is of the steady state).  ``roofline`` is for that step's only
 kernel (w4a16_pf, the direct-to-LDS prefill GEMM), its average duration
 taken from HIP events on the stream it is launched on; ``traffic`` is the
 HBM bytes per launch measured with rocprofv3 counters (FETCH_SIZE and
@@ -63,9 +66,31 @@ def randn_bf16(seed, shape):
     return torch.randn(shape, generator=g).to(torch.bfloat16).cuda()
 
 
-def time_eager(fn, steps, warmup):
-    """(wall ms per step, HIP-event ms per step) over `steps` calls."""
+RAMP_MS = 40.0
+
+
+def ramp_clocks(fn, ms=RAMP_MS):
+    """Call fn back to back for `ms` of wall time, untimed.  After an idle
+    spell MI355X raises its clocks over the first ~10-15 ms of sustained
+    work (measured on the headline kernel: ~86 us per launch for the first
+    20 launches, ~78 us from about the 140th on, flat for the next 0.5 s),
+    so timing right after start-up measures the ramp, not the kernel."""
     import torch
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        fn()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
+def time_eager(fn, steps, warmup):
+    """(wall ms per step, HIP-event ms per step) over `steps` calls, after
+    the clock ramp and `warmup` untimed calls."""
+    import torch
+    ramp_clocks(fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -96,8 +121,7 @@ def time_graph(fns, replays=20):
             for f in fns:
                 f()
     torch.cuda.current_stream().wait_stream(s)
-    g.replay()
-    torch.cuda.synchronize()
+    ramp_clocks(g.replay)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -336,8 +360,8 @@ def cpu_baseline(np, m, k, n, budget_s=20.0):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -366,7 +390,9 @@ def main() -> int:
     rng = np.random.default_rng(20260810 + 1)
     (w, s), = rand_weights(rng, (n,), k)
     x = randn_bf16(20260810, (m, k))
-    log(f"headline: w4a16 linear m={m} k={k} n={n}, warmup {args.warmup}, steps {args.steps}")
+    log(f"headline: w4a16 linear m={m} k={k} n={n}, clock ramp {RAMP_MS:.0f} ms, "
+        f"warmup {args.warmup}, steps {args.steps}")
+    ramp_clocks(lambda: mx.linear_mxfp4_soft(x, w, s))
     for _ in range(args.warmup):
         mx.linear_mxfp4_soft(x, w, s)
     torch.cuda.synchronize()

@@ -90,6 +90,36 @@ __device__ __forceinline__ int64_t rows_in_use(const GemmArgs& g) {
   return npp < g.m ? npp : g.m;
 }
 
+// Tile order of the direct-to-LDS kernels; workgroup i runs on XCD i % 8.
+// Dense: each XCD gets a contiguous range of tiles, walked in groups of 4
+// row blocks, keeping its A rows and B columns L2-resident.  Routed: the
+// grid covers the capacity of sorted_ids (nbm rounded up to a multiple of
+// 8) but only the first ceil(num_post_padded / bm_rows) row blocks are
+// live; those are split into 8 contiguous ranges of equal size, one per
+// XCD, each XCD walking all column tiles of a row block before the next.
+// Consecutive row blocks mostly belong to one expert, so an expert's
+// weights are fetched into few L2s, and every XCD gets an equal share of
+// the live rows.  Returns false for workgroups past the live range.
+__device__ __forceinline__ bool tile_of(const GemmArgs& g, int bm_rows, int nbm, int nbn, int& bm,
+                                        int& bn) {
+  const int x = blockIdx.x % 8, i = blockIdx.x / 8;
+  if (g.sorted_ids) {
+    const int live = (int)((rows_in_use(g) + bm_rows - 1) / bm_rows);
+    const int lo = (int)((int64_t)live * x / 8), hi = (int)((int64_t)live * (x + 1) / 8);
+    bm = lo + i / nbn;
+    bn = i % nbn;
+    return bm < hi;
+  }
+  const int nwg = gridDim.x, per = nwg / 8, rem = nwg % 8;
+  const int pid = x * per + (x < rem ? x : rem) + i;
+  constexpr int GROUP = 4;
+  const int first_m = (pid / (GROUP * nbn)) * GROUP;
+  const int gsize = (nbm - first_m) < GROUP ? (nbm - first_m) : GROUP;
+  bm = first_m + (pid % (GROUP * nbn)) % gsize;
+  bn = (pid % (GROUP * nbn)) / gsize;
+  return (int64_t)bm * bm_rows < g.m;
+}
+
 __device__ __forceinline__ float scalar_alpha(const GemmArgs& g, int expert) {
   float a = g.a_scale ? g.a_scale[0] : 1.0f;
   if (g.b_scale) a *= g.b_scale[expert];
@@ -100,10 +130,9 @@ __device__ __forceinline__ float scalar_alpha(const GemmArgs& g, int expert) {
 int launch_w4a16(const GemmArgs& g, int dtype, int epi, hipStream_t st);
 // Direct-to-LDS prefill kernel (gemm_w4a16_pf.hip): tile configurations.
 enum PfConfig {
-  PF_128x256 = 0,  // 1 x 8 waves of 128 x 32
-  PF_128x128 = 1,  // 1 x 4 waves of 128 x 32
-  PF_64x128 = 2,   // 1 x 4 waves of 64 x 32, 3 stages
-  PF_32x128 = 3,   // 1 x 4 waves of 32 x 32, 3 stages
+  PF_128x128 = 0,  // 1 x 4 waves of 128 x 32
+  PF_64x128 = 1,   // 1 x 4 waves of 64 x 32, 3 stages
+  PF_32x128 = 2,   // 1 x 4 waves of 32 x 32, 3 stages
 };
 bool pf_supported(const GemmArgs& g, int elem_bytes);
 int pf_choose(const GemmArgs& g, int epi);

@@ -21,9 +21,8 @@
 // * Epilogue.  Scales / route weight / bias / SiLU*mul are applied in
 //   registers, the tile is staged in LDS (reusing the stage buffers) and
 //   written back as full 16-byte chunks, whole output rows per instruction.
-// * Order.  Tiles are remapped so each XCD (workgroups are dealt round-robin
-//   over the 8 XCDs) gets a contiguous range, walked in groups of 4 row
-//   blocks, keeping each XCD's A rows and B columns L2-resident.
+// * Order.  Workgroups are dealt round-robin over the 8 XCDs; tile_of
+//   (gemm.h) gives each XCD a contiguous range of rows.
 //
 // Requirements (else the host falls back to the register-staged kernel):
 // K % 128 == 0; activation and weight byte ranges below 2 GiB; 16-byte
@@ -98,32 +97,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   const int c16 = lane & 15;
   const int grp = lane >> 4;
 
-  // ---- tile order.  Workgroup i runs on XCD i % 8.  Dense: each XCD gets a
-  // contiguous range of tiles, walked in groups of 4 row blocks, keeping
-  // its A rows and B columns L2-resident.  Routed: the grid covers the
-  // capacity of sorted_ids and only the first num_post_padded rows are
-  // live, so contiguous ranges would leave the XCDs holding the tail idle;
-  // instead row blocks are dealt round-robin over the XCDs (the host pads
-  // the row-block count to a multiple of 8), each XCD walking all column
-  // tiles of one row block (one expert's weights, shared A rows) at a time.
   int bm, bn;
-  if (g.sorted_ids) {
-    const int x = blockIdx.x % 8, i = blockIdx.x / 8;
-    bm = x + 8 * (i / nbn);
-    bn = i % nbn;
-  } else {
-    int pid = blockIdx.x;
-    const int nwg = gridDim.x, per = nwg / 8, rem = nwg % 8, x = pid % 8, i = pid / 8;
-    pid = x * per + (x < rem ? x : rem) + i;
-    constexpr int GROUP = 4;
-    const int first_m = (pid / (GROUP * nbn)) * GROUP;
-    const int gsize = (nbm - first_m) < GROUP ? (nbm - first_m) : GROUP;
-    bm = first_m + (pid % (GROUP * nbn)) % gsize;
-    bn = (pid % (GROUP * nbn)) / gsize;
-  }
-
+  if (!tile_of(g, BM, nbm, nbn, bm, bn)) return;
   const int64_t pos0 = (int64_t)bm * BM;
-  if (pos0 >= rows_in_use(g)) return;
   const int expert = g.sorted_ids ? block_expert(g, pos0) : 0;
   const int ncol0 = bn * OUT_COLS;
 
@@ -359,7 +335,7 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int out_cols = (EPI == EPI_SILU_MUL) ? S::BN / 2 : S::BN;
   const int nbn = (g.n + out_cols - 1) / out_cols;
   int64_t nbm = (g.m + S::BM - 1) / S::BM;
-  if (g.sorted_ids) nbm = (nbm + 7) / 8 * 8;  // row blocks dealt over 8 XCDs
+  if (g.sorted_ids) nbm = (nbm + 7) / 8 * 8;  // every XCD covers 1/8 of the capacity (tile_of)
   const int64_t nwg = nbm * nbn;
   if (nwg <= 0 || nwg > 0x7FFFFFFF) {
     set_error("w4a16 prefill: bad grid");
@@ -374,20 +350,23 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 // stages, workgroups per CU).  Every configuration puts its waves side by
 // side on columns (WGM = 1): a wave then spans all BM rows, so each decoded
 // weight fragment feeds BM / 16 MFMAs and the per-MFMA decode work is the
-// smallest the tile allows (measured +2-7% at 128 rows, +13-15% at 32-64
-// rows against 2 x 2 waves).  Medians of interleaved MI355X runs (bf16):
-// 128 x 128 for M = 4096 at qkv / o_proj shapes, 128 x 256 (8 waves) once
-// there are >= 2048 128 x 128 tiles (M 8192 K N 4096: +5%), 64 x 128 and
-// 32 x 128 (3 stages) for mid M (M ~ 1024 and ~ 370, and MoE blocks of 64).
-// Rejected: 256 x 160, 128 x 320, 256 x 256, 128 x 512, 192 x 256, 64 x
-// 256/512, 32 x 256/512, wave tiles of 128 x 64 (2 or 4 waves), 128 x
-// 160 / 128 x 320 (5 / 10 waves: a wave count that is not a multiple of
-// the 4 SIMDs loads one SIMD twice), and 3-4 stages at 128 rows (the extra LDS or registers cost more occupancy than
-// the deeper pipeline or the fewer LDS reads gain).
+// smallest the tile allows (+2-7% at 128 rows, +13-15% at 32-64 rows
+// against 2 x 2 waves).  Measured at steady clocks on MI355X (bf16):
+// 128 x 128 for M >= ~2048 (qkv and o_proj at M = 4096, M = 8192 K = N =
+// 4096, the MoE layer at 4096 tokens), 64 x 128 and 32 x 128 (3 stages) for
+// mid M (M ~ 1024 and ~ 370, and MoE blocks of 64).  Rejected: 128 x 256
+// with 8 waves (1150 vs 1183 TFLOP/s at M = 8192 K = N = 4096; MoE layer
+// at 4096 tokens 496 vs 454 us), 128 x 160 with 2 x 2 waves of 64 x 80
+// (1029-1107 vs 994-1099 TFLOP/s over M = 3072-6144 at qkv: no steady
+// gain), 256 x 160, 128 x 320, 256 x 256, 128 x 512, 192 x 256, 64 x
+// 256/512, 32 x 256/512, wave tiles of 128 x 64, 5 or 10 waves (a wave
+// count that is not a multiple of the 4 SIMDs loads one SIMD twice), 3-4
+// stages at 128 rows (the extra LDS costs a workgroup per CU: -10-20% for
+// the routed GEMMs), and weights prefetched 2-4 stages ahead of the
+// activations (no gain: the routed GEMMs wait on activation rows as much).
 template <typename T, int EPI>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
-    case PF_128x256: return launch_cfg<T, 1, 8, 8, 2, 2, EPI, 1>(g, st);
     case PF_128x128: return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2>(g, st);
     case PF_64x128: return launch_cfg<T, 1, 4, 4, 2, 3, EPI, 4>(g, st);
     default: return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4>(g, st);
@@ -416,7 +395,6 @@ int pf_choose(const GemmArgs& g, int epi) {
     return ((g.m + bm - 1) / bm) * (int64_t)((g.n + out - 1) / out);
   };
   if (allowed(128)) {
-    if (tiles(128, 128) >= 2048) return PF_128x256;
     if (tiles(128, 128) >= 512) return PF_128x128;
   }
   if (allowed(64) && tiles(64, 128) >= 512) return PF_64x128;

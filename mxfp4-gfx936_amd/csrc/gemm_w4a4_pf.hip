@@ -90,26 +90,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
   const int c16 = lane & 15;
   const int grp = lane >> 4;
 
-  // tile order as in the W4A16 prefill kernel: dense grids give each XCD a
-  // contiguous range in groups of 4 row blocks; routed grids deal row
-  // blocks round-robin over the 8 XCDs
   int bm, bn;
-  if (g.sorted_ids) {
-    const int x = blockIdx.x % 8, i = blockIdx.x / 8;
-    bm = x + 8 * (i / nbn);
-    bn = i % nbn;
-  } else {
-    int pid = blockIdx.x;
-    const int nwg = gridDim.x, per = nwg / 8, rem = nwg % 8, x = pid % 8, i = pid / 8;
-    pid = x * per + (x < rem ? x : rem) + i;
-    constexpr int GROUP = 4;
-    const int first_m = (pid / (GROUP * nbn)) * GROUP;
-    const int gsize = (nbm - first_m) < GROUP ? (nbm - first_m) : GROUP;
-    bm = first_m + (pid % (GROUP * nbn)) % gsize;
-    bn = (pid % (GROUP * nbn)) / gsize;
-  }
+  if (!tile_of(g, BM, nbm, nbn, bm, bn)) return;
   const int64_t pos0 = (int64_t)bm * BM;
-  if (pos0 >= rows_in_use(g)) return;
   const int expert = g.sorted_ids ? block_expert(g, pos0) : 0;
   const int ncol0 = bn * BN;
 
@@ -303,7 +286,7 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
   typedef P4Shape<WGM, WGN, FM, FN, STAGES> S;
   const int nbn = (g.n + S::BN - 1) / S::BN;
   int64_t nbm = (g.m + S::BM - 1) / S::BM;
-  if (g.sorted_ids) nbm = (nbm + 7) / 8 * 8;  // row blocks dealt over 8 XCDs
+  if (g.sorted_ids) nbm = (nbm + 7) / 8 * 8;  // every XCD covers 1/8 of the capacity (tile_of)
   const int64_t nwg = nbm * nbn;
   if (nwg <= 0 || nwg > 0x7FFFFFFF) {
     set_error("w4a4 prefill: bad grid");
@@ -349,9 +332,12 @@ int p4_choose(const GemmArgs& g, int out_dtype) {
   const bool routed = g.sorted_ids != nullptr;
   auto allowed = [&](int bm) { return !routed || g.block_m % bm == 0; };
   auto tiles = [&](int bm, int bn) { return ((g.m + bm - 1) / bm) * (int64_t)((g.n + bn - 1) / bn); };
-  // FP32 output stages 4-byte rows: keep its epilogue within 128 x 128
+  // FP32 output stages 4-byte rows: keep its epilogue within 128 x 128.
+  // 256 x 256 needs a tile for every CU (steady clocks, bf16 out: 2.99 vs
+  // 2.06 PFLOP/s at M = 8192 K = N = 4096 with 512 tiles; with 160 tiles,
+  // M = 2048 K = 2048 N = 5120, 128 x 128 wins 1.69 vs 1.59).
   const bool wide = out_dtype != MXFP4_DT_F32;
-  if (wide && allowed(256) && tiles(256, 256) >= 128) return P4_256x256;
+  if (wide && allowed(256) && tiles(256, 256) >= 256) return P4_256x256;
   if (allowed(128) && tiles(128, 128) >= 128) return P4_128x128;
   if (allowed(64)) return P4_64x128;
   return -1;

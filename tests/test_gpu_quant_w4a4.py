@@ -59,12 +59,12 @@ def test_w4a4_linear(m, k, n, out_dtype):
     del rng
 
 
-@pytest.mark.parametrize("m,n,out_dtype", [(2048, 4096, torch.bfloat16), (2048, 2048, torch.float16),
+@pytest.mark.parametrize("m,n,out_dtype", [(4096, 4096, torch.bfloat16), (2048, 2048, torch.float16),
                                            (2048, 4096, torch.float32), (1000, 4100, torch.bfloat16)],
-                         ids=["128x256", "128x128", "f32_out", "partial"])
+                         ids=["256x256", "128x128", "f32_out", "partial"])
 def test_w4a4_tile_configs(m, n, out_dtype):
-    # grids large enough for the 128 x 256 / 128 x 128 tiles, FP32 output,
-    # and partial row / column tiles; checked on sampled rows
+    # grids large enough for the 256 x 256 (>= 256 tiles) / 128 x 128 tiles,
+    # FP32 output, and partial row / column tiles; checked on sampled rows
     k = 256
     a = rand_act(m + 1, (m, k)).float().numpy()
     w = (rand_act(n + 2, (n, k)).float() * 0.02).numpy()
