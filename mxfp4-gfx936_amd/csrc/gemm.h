@@ -130,9 +130,10 @@ __device__ __forceinline__ float scalar_alpha(const GemmArgs& g, int expert) {
 int launch_w4a16(const GemmArgs& g, int dtype, int epi, hipStream_t st);
 // Direct-to-LDS prefill kernel (gemm_w4a16_pf.hip): tile configurations.
 enum PfConfig {
-  PF_128x128 = 0,  // 1 x 4 waves of 128 x 32
-  PF_64x128 = 1,   // 1 x 4 waves of 64 x 32, 3 stages
-  PF_32x128 = 2,   // 1 x 4 waves of 32 x 32, 3 stages
+  PF_128x256 = 0,  // 1 x 4 waves of 128 x 64
+  PF_128x128 = 1,  // 1 x 4 waves of 128 x 32
+  PF_64x128 = 2,   // 1 x 4 waves of 64 x 32, 3 stages
+  PF_32x128 = 3,   // 1 x 4 waves of 32 x 32, 3 stages
 };
 bool pf_supported(const GemmArgs& g, int elem_bytes);
 int pf_choose(const GemmArgs& g, int epi);

@@ -352,21 +352,27 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 // weight fragment feeds BM / 16 MFMAs and the per-MFMA decode work is the
 // smallest the tile allows (+2-7% at 128 rows, +13-15% at 32-64 rows
 // against 2 x 2 waves).  Measured at steady clocks on MI355X (bf16):
-// 128 x 128 for M >= ~2048 (qkv and o_proj at M = 4096, M = 8192 K = N =
-// 4096, the MoE layer at 4096 tokens), 64 x 128 and 32 x 128 (3 stages) for
-// mid M (M ~ 1024 and ~ 370, and MoE blocks of 64).  Rejected: 128 x 256
-// with 8 waves (1150 vs 1183 TFLOP/s at M = 8192 K = N = 4096; MoE layer
-// at 4096 tokens 496 vs 454 us), 128 x 160 with 2 x 2 waves of 64 x 80
-// (1029-1107 vs 994-1099 TFLOP/s over M = 3072-6144 at qkv: no steady
-// gain), 256 x 160, 128 x 320, 256 x 256, 128 x 512, 192 x 256, 64 x
-// 256/512, 32 x 256/512, wave tiles of 128 x 64, 5 or 10 waves (a wave
-// count that is not a multiple of the 4 SIMDs loads one SIMD twice), 3-4
-// stages at 128 rows (the extra LDS costs a workgroup per CU: -10-20% for
-// the routed GEMMs), and weights prefetched 2-4 stages ahead of the
-// activations (no gain: the routed GEMMs wait on activation rows as much).
+// 128 x 256 (waves of 128 x 64: per MFMA half the activation bytes of
+// 128 x 128) once there are >= 1024 such tiles (M = 8192 K = N = 4096:
+// 1310 vs 1212 TFLOP/s, M = 8192 K = 2048 N = 5120: 1258 vs 1198, MoE
+// down at 4096 tokens -3%), 128 x 128 below that (qkv at M = 4096, 640
+// wide tiles on 512 workgroup slots: 1128 vs 1044), 64 x 128 and 32 x 128
+// (3 stages) for mid M (M ~ 1024 and ~ 370, and MoE blocks of 64).
+// Rejected: 128 x 256 with 8 waves of 128 x 32 (1150 vs 1183 TFLOP/s at
+// M = 8192 K = N = 4096; MoE layer at 4096 tokens 496 vs 454 us); 256 x
+// 160 and 256 x 128 of 2 x 2 waves (128 x 80 / 128 x 64: slower than the
+// better of the two above at both sizes); 128 x 192 and 3-stage 128 x 256
+// (slower at every size); 128 x 160 of 2 x 2 waves of 64 x 80 (no steady
+// gain over M = 3072-6144 at qkv); 128 x 320, 256 x 256, 128 x 512, 192 x
+// 256, 64 x 256/512, 32 x 256/512; 5 or 10 waves (a wave count that is not
+// a multiple of the 4 SIMDs loads one SIMD twice); 3-4 stages at 128 rows
+// (the extra LDS costs a workgroup per CU: -10-20% for the routed GEMMs);
+// weights prefetched 2-4 stages ahead of the activations (no gain: the
+// routed GEMMs wait on activation rows as much).
 template <typename T, int EPI>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
+    case PF_128x256: return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2>(g, st);
     case PF_128x128: return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2>(g, st);
     case PF_64x128: return launch_cfg<T, 1, 4, 4, 2, 3, EPI, 4>(g, st);
     default: return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4>(g, st);
@@ -395,6 +401,7 @@ int pf_choose(const GemmArgs& g, int epi) {
     return ((g.m + bm - 1) / bm) * (int64_t)((g.n + out - 1) / out);
   };
   if (allowed(128)) {
+    if (tiles(128, 256) >= 1024) return PF_128x256;
     if (tiles(128, 128) >= 512) return PF_128x128;
   }
   if (allowed(64) && tiles(64, 128) >= 512) return PF_64x128;
