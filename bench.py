@@ -430,7 +430,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                      "traffic": recorded_traffic(),
-                     "kernel": "w4a16_pf<bf16> 128x128 tile (direct-to-LDS)",
+                     "kernel": "w4a16_pf<bf16> 128x320 tile, 4 waves of 128x80 (direct-to-LDS)",
                      "kernel_us": round(kernel_ms * 1e3, 3),
                      "algorithmic_bytes": linear_bytes(m, n, k)},
     }

@@ -134,6 +134,7 @@ enum PfConfig {
   PF_128x128 = 1,  // 1 x 4 waves of 128 x 32
   PF_64x128 = 2,   // 1 x 4 waves of 64 x 32, 3 stages
   PF_32x128 = 3,   // 1 x 4 waves of 32 x 32, 3 stages
+  PF_128x320 = 4,  // 1 x 4 waves of 128 x 80 (plain store epilogue only)
 };
 bool pf_supported(const GemmArgs& g, int elem_bytes);
 int pf_choose(const GemmArgs& g, int epi);

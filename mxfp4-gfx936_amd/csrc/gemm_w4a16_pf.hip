@@ -60,6 +60,7 @@ struct PfShape {
   static constexpr int A_TOT = BM / 8;      // 1 KB wave-loads per stage (8 rows each)
   static constexpr int B_TOT = BN / 32;     // (32 rows each)
   static constexpr int S_TOT = (BN + 63) / 64;  // scale wave-loads (64 rows x 4 bytes)
+  static constexpr int S_PER = (S_TOT + NW - 1) / NW;
   static constexpr int A_PER = (A_TOT + NW - 1) / NW;
   static constexpr int B_PER = (B_TOT + NW - 1) / NW;
   static constexpr bool EVEN = A_TOT % NW == 0 && B_TOT % NW == 0;
@@ -69,6 +70,15 @@ struct PfShape {
   static constexpr int PIPE = STAGES * (A_STAGE + B_STAGE) + S_SLOTS * S_SLOT;
 };
 
+// The finished tile is staged in LDS (reusing the pipeline buffers) in as
+// few row passes as fit: the smallest power of two P, keeping BM / P a
+// multiple of 16, with (BM / P) * row_bytes <= pipe_bytes.
+constexpr int epi_passes(int bm, int row_bytes, int pipe_bytes) {
+  int p = 1;
+  while ((bm / p) * row_bytes > pipe_bytes && (bm / p) % 32 == 0) p *= 2;
+  return p;
+}
+
 template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB>
 __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int nbm, int nbn) {
   typedef typename V8Of<T>::type V8;
@@ -76,12 +86,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
   constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int C_LD = OUT_COLS * 2 + 16;  // bytes per staged output row
-  // the finished tile is staged in LDS whole, or one wave row at a time
-  // when that would not fit in the pipeline buffers
-  constexpr int EPI_PASSES = BM * C_LD <= S::PIPE ? 1 : WGM;
+  constexpr int EPI_PASSES = epi_passes(BM, C_LD, S::PIPE);
   constexpr int EPI_ROWS = BM / EPI_PASSES;
   constexpr int SMEM = S::PIPE > EPI_ROWS * C_LD ? S::PIPE : EPI_ROWS * C_LD;
-  static_assert(S::S_TOT <= S::NW && BN % 32 == 0, "tile config");
+  static_assert(BN % 32 == 0 && EPI_ROWS % 16 == 0, "tile config");
   static_assert(STAGES == 2 || S::EVEN, "multi-stage waits count loads per wave");
   static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 stages");
   static_assert(EPI != EPI_SILU_MUL || FN % 2 == 0, "SiLU pairs need even FN");
@@ -160,18 +168,26 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     const int grow = q < S::B_TOT ? weight_row(row) : -1;
     b_off[j] = grow >= 0 ? (uint32_t)(grow * g.b_n) + c * 16 : kOOB;
   }
-  uint32_t s_off = kOOB;
-  if (wave < S::S_TOT) {
-    const int grow = weight_row(wave * 64 + lane);
-    s_off = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
+  uint32_t s_off[S::S_PER];
+#pragma unroll
+  for (int j = 0; j < S::S_PER; ++j) {
+    const int q = j * S::NW + wave;
+    const int grow = q < S::S_TOT ? weight_row(q * 64 + lane) : -1;
+    s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
   }
 
   const int nk = g.k / 64;
   auto issue = [&](int kt) {
     const int st = kt % STAGES;
-    if ((kt & 1) == 0 && wave < S::S_TOT)
-      llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + wave * 256),
-                                      4, (int)s_off, (kt >> 1) * 4, 0, 0);
+    if ((kt & 1) == 0) {
+#pragma unroll
+      for (int j = 0; j < S::S_PER; ++j) {
+        const int q = j * S::NW + wave;
+        if (q < S::S_TOT)
+          llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + q * 256),
+                                          4, (int)s_off[j], (kt >> 1) * 4, 0, 0);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < S::A_PER; ++j) {
       const int q = j * S::NW + wave;
@@ -260,9 +276,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   const float alpha = scalar_alpha(g, expert);
 #pragma unroll
   for (int pass = 0; pass < EPI_PASSES; ++pass) {
-    if (EPI_PASSES == 1 || wm == pass) {
+    {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
+        if ((wm * FM * 16 + fm * 16) / EPI_ROWS != pass) continue;  // another pass's rows
         const int trow = wm * FM * 16 + fm * 16 + c16;
         float rw = 1.0f;
         if (g.route_w) {
@@ -351,13 +368,18 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 // side on columns (WGM = 1): a wave then spans all BM rows, so each decoded
 // weight fragment feeds BM / 16 MFMAs and the per-MFMA decode work is the
 // smallest the tile allows (+2-7% at 128 rows, +13-15% at 32-64 rows
-// against 2 x 2 waves).  Measured at steady clocks on MI355X (bf16):
-// 128 x 256 (waves of 128 x 64: per MFMA half the activation bytes of
-// 128 x 128) once there are >= 1024 such tiles (M = 8192 K = N = 4096:
-// 1310 vs 1212 TFLOP/s, M = 8192 K = 2048 N = 5120: 1258 vs 1198, MoE
-// down at 4096 tokens -3%), 128 x 128 below that (qkv at M = 4096, 640
-// wide tiles on 512 workgroup slots: 1128 vs 1044), 64 x 128 and 32 x 128
-// (3 stages) for mid M (M ~ 1024 and ~ 370, and MoE blocks of 64).
+// against 2 x 2 waves).  Measured at steady clocks on MI355X (bf16): the
+// wide tiles 128 x 256 and 128 x 320 (waves of 128 x 64 / 128 x 80: per
+// MFMA 1/2 and 2/5 of the activation LDS bytes of 128 x 128) run two
+// workgroups per CU, so they pay off when their tiles fill whole rounds of
+// the 512 slots: M = 8192 K = N = 4096 (1024 tiles of 128 x 256): 1310 vs
+// 1212 TFLOP/s; M = K = N = 4096 (512): -6%; qkv M = 4096 (512 tiles of
+// 128 x 320): -3%; M = 8192 K = 2048 N = 5120 (1024 of 128 x 320): -4%;
+// MoE down at 4096 tokens: -3%.  With 640 tiles of 128 x 256 (qkv M =
+// 4096) or 800 (N = 6400) they lose 4-6% to 128 x 128 (three per CU), and
+// below 512 tiles more.  pf_choose takes the wide tile whose rounds are
+// >= 80% full, else 128 x 128; 64 x 128 and 32 x 128 (3 stages) for mid M
+// (M ~ 1024 and ~ 370, and MoE blocks of 64).
 // Rejected: 128 x 256 with 8 waves of 128 x 32 (1150 vs 1183 TFLOP/s at
 // M = 8192 K = N = 4096; MoE layer at 4096 tokens 496 vs 454 us); 256 x
 // 160 and 256 x 128 of 2 x 2 waves (128 x 80 / 128 x 64: slower than the
@@ -372,6 +394,9 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 template <typename T, int EPI>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
+    case PF_128x320:
+      if constexpr (EPI == EPI_STORE) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2>(g, st);
+      else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2>(g, st);  // SiLU pairs need even FN
     case PF_128x256: return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2>(g, st);
     case PF_128x128: return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2>(g, st);
     case PF_64x128: return launch_cfg<T, 1, 4, 4, 2, 3, EPI, 4>(g, st);
@@ -400,8 +425,18 @@ int pf_choose(const GemmArgs& g, int epi) {
     const int out = epi == EPI_SILU_MUL ? bn / 2 : bn;
     return ((g.m + bm - 1) / bm) * (int64_t)((g.n + out - 1) / out);
   };
+  // share of the 512 workgroup slots (two per CU) that a wide tile keeps
+  // busy over all its rounds; 0 below one full round
+  auto fill = [&](int bn) {
+    const int64_t t = tiles(128, bn);
+    const int64_t rounds = (t + 511) / 512;
+    return t >= 512 ? (double)t / (double)(rounds * 512) : 0.0;
+  };
   if (allowed(128)) {
-    if (tiles(128, 256) >= 1024) return PF_128x256;
+    const double f256 = fill(256);
+    const double f320 = epi == EPI_STORE ? fill(320) : 0.0;
+    if (f320 >= 0.8 && f320 >= f256) return PF_128x320;
+    if (f256 >= 0.8) return PF_128x256;
     if (tiles(128, 128) >= 512) return PF_128x128;
   }
   if (allowed(64) && tiles(64, 128) >= 512) return PF_64x128;

@@ -117,8 +117,9 @@ def test_linear_attention_shapes(m, k, n):
 @pytest.mark.parametrize("m,k,n", [(8192, 4096, 4096), (2100, 256, 16400)],
                          ids=["cube", "partial_tiles"])
 def test_linear_wide_tile_shapes(m, k, n):
-    # large grids (2048 tiles of 128 x 128, 8 per CU); the second shape ends
-    # in a partial row tile and a 16-column last tile
+    # the wide tiles: 1024 tiles of 128 x 256 (two full rounds of two per
+    # CU), and 128 x 320 tiles ending in a partial row tile and an 80-column
+    # last tile
     rng = np.random.default_rng(20261201 + m)
     packed, scales = rand_mxfp4(rng, (n,), k)
     x = rand_act(20261201 + n, (m, k))
