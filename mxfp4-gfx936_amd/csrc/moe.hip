@@ -52,55 +52,86 @@ __global__ __launch_bounds__(256) void align_count(const TI* __restrict__ ids, i
     counts[(int64_t)blockIdx.x * num_experts + e] = hist[e];
 }
 
+// One 1024-thread workgroup; thread e owns expert e.  Chunk counts are
+// loaded kScanBatch at a time (one memory round trip each; the first
+// batch's prefixes are kept in registers until the start is known), the padded
+// expert totals are scanned with wave shuffles plus the 16 wave sums, and
+// the sentinel padding and expert_ids are written by whole waves (an
+// expert's padding is < block_m entries: at most two per lane).
+constexpr int kScanBatch = 32;
+
 __global__ __launch_bounds__(1024) void align_scan(int32_t* __restrict__ counts, int nchunks,
                                                    int num_experts, int block_m, int64_t n,
                                                    int32_t* __restrict__ sorted_ids,
                                                    int32_t* __restrict__ expert_ids,
                                                    int32_t* __restrict__ num_post_padded) {
-  __shared__ int scan[kMaxExperts];
+  __shared__ int wsum[kMaxExperts / 64];
+  __shared__ int s_start[kMaxExperts], s_total[kMaxExperts], s_pad[kMaxExperts];
   const int e = threadIdx.x;
-  // exclusive prefix over chunks within the expert, eight chunks' counts
-  // loaded before any is rewritten (one memory round trip per 8 chunks)
+  const int lane = e & 63, wave = e >> 6;
+  // exclusive prefix over chunks within the expert; the first batch's
+  // prefixes stay in registers, later batches go back to memory
   int total = 0;
+  int pre[kScanBatch];
   if (e < num_experts) {
-    for (int b0 = 0; b0 < nchunks; b0 += 8) {
-      int c[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < kScanBatch; ++j)
+      pre[j] = j < nchunks ? counts[(int64_t)j * num_experts + e] : 0;
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) {
+      const int c = pre[j];
+      pre[j] = total;
+      total += c;
+    }
+    for (int b0 = kScanBatch; b0 < nchunks; b0 += kScanBatch) {
+      int c[kScanBatch];
+#pragma unroll
+      for (int j = 0; j < kScanBatch; ++j)
         c[j] = b0 + j < nchunks ? counts[(int64_t)(b0 + j) * num_experts + e] : 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < kScanBatch; ++j)
         if (b0 + j < nchunks) {
           counts[(int64_t)(b0 + j) * num_experts + e] = total;
           total += c[j];
         }
     }
   }
-  const int padded = ((total + block_m - 1) / block_m) * block_m;
-  scan[e] = (e < num_experts) ? padded : 0;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over 1024 entries
-  for (int off = 1; off < kMaxExperts; off <<= 1) {
-    const int v = (e >= off) ? scan[e - off] : 0;
-    __syncthreads();
-    scan[e] += v;
-    __syncthreads();
-  }
-  const int start = scan[e] - padded;  // exclusive
-  if (e < num_experts) {
-    for (int b0 = 0; b0 < nchunks; b0 += 8) {
-      int c[8];
+  const int padded = e < num_experts ? ((total + block_m - 1) / block_m) * block_m : 0;
+  // inclusive scan of the padded totals over experts
+  int v = padded;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off);
+    if (lane >= off) v += u;
+  }
+  if (lane == 63) wsum[wave] = v;
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) v += wsum[w];
+  const int start = v - padded;  // exclusive
+  if (e < num_experts) {
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j)
+      if (j < nchunks) counts[(int64_t)j * num_experts + e] = pre[j] + start;
+    for (int b0 = kScanBatch; b0 < nchunks; b0 += kScanBatch) {
+      int c[kScanBatch];
+#pragma unroll
+      for (int j = 0; j < kScanBatch; ++j)
         c[j] = b0 + j < nchunks ? counts[(int64_t)(b0 + j) * num_experts + e] : 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < kScanBatch; ++j)
         if (b0 + j < nchunks) counts[(int64_t)(b0 + j) * num_experts + e] = c[j] + start;
     }
-    for (int blk = start / block_m; blk < (start + padded) / block_m; ++blk) expert_ids[blk] = e;
-    for (int p = start + total; p < start + padded; ++p) sorted_ids[p] = (int32_t)n;
+    s_start[e] = start;
+    s_total[e] = total;
+    s_pad[e] = padded;
   }
-  if (e == kMaxExperts - 1) num_post_padded[0] = scan[e];
+  if (e == num_experts - 1) num_post_padded[0] = v;
+  __syncthreads();
+  for (int x = wave; x < num_experts; x += kMaxExperts / 64) {
+    const int st = s_start[x], end = st + s_pad[x];
+    for (int i = lane; i < s_pad[x] / block_m; i += 64) expert_ids[st / block_m + i] = x;
+    for (int p = st + s_total[x] + lane; p < end; p += 64) sorted_ids[p] = (int32_t)n;
+  }
 }
 
 template <typename TI>
