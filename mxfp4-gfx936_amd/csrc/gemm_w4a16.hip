@@ -397,6 +397,220 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------- stream
+// Single-trip decode (one 16-row block; every wave's K slice is one trip of
+// U 128-K units) over CS steps of WN groups of 16 output columns.  The
+// workgroup looks up its rows and stages its activation rows once, then
+// software-pipelines the steps: the weights and scales of step s + 1 are in
+// flight while step s is decoded, multiplied, reduced across the WK waves
+// (double-buffered LDS, one barrier per step) and stored.  For grids of
+// many small workgroups (routed decode: an expert block times a column
+// group each) this pays the row lookup and the first memory round trip
+// once per CS column groups, and keeps weight loads streaming through the
+// epilogues.  Same loads, rounding and reduction order as the skinny
+// kernel, so results are identical.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <typename T, int WK, int WN, int U, int CS, int EPI>
+__global__ __launch_bounds__(WK * WN * 64) void w4a16_stream(GemmArgs g) {
+  typedef typename V8Of<T>::type V8;
+  constexpr int NB = (EPI == EPI_SILU_MUL) ? 2 : 1;
+  static_assert(U == 2 || U == 4, "scale loads cover 2 or 4 units");
+  __shared__ f32x4 red[2][WK][WN][NB][64];
+  __shared__ int64_t srow[16];
+  extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // staged activation rows
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wk = wave % WK;
+  const int wn = wave / WK;
+  const int c16 = lane & 15;
+  const int grp = lane >> 4;
+  // the row lookup of the skinny kernel for one 16-row block
+  const int64_t pos0 = (int64_t)blockIdx.y * 16;
+  int expert = 0;
+  int64_t my_route[1];
+  if (g.route_ids) {
+    if (direct_rows<1>(g, (int)blockIdx.y, c16, &expert, my_route)) return;
+  } else if (g.sorted_ids) {
+    const int64_t npp = *g.num_post_padded;
+    const int e = block_expert(g, pos0);
+    if (pos0 >= (npp < g.m ? npp : g.m)) return;
+    expert = e;
+    const RowInfo ri = row_info(g, pos0 + c16);
+    my_route[0] = ri.valid ? ri.out_row : -1;
+  } else {
+    if (pos0 >= g.m) return;
+    my_route[0] = pos0 + c16 < g.m ? pos0 + c16 : -1;
+  }
+  if (wave == 0 && grp == 0) srow[c16] = my_route[0];
+  // first output column of wave-column w at step s
+  auto col0 = [&](int s, int w) { return (((int)blockIdx.x * CS + s) * WN + w) * 16; };
+
+  if (expert < 0) {  // aiter:156-172: expert not on this device -> zeros
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < CS * WN * 256; idx += WK * WN * 64) {
+      const int s = idx / (WN * 256), w = (idx >> 8) % WN;
+      const int col = col0(s, w) + ((idx >> 2) & 15);
+      const int64_t row = srow[((idx >> 6) & 3) * 4 + (idx & 3)];
+      if (row >= 0 && col < g.n) static_cast<T*>(g.c)[row * g.ldc + col] = from_f32<T>(0.f);
+    }
+    return;
+  }
+
+  const int64_t b_rows_total = (NB == 2) ? 2 * (int64_t)g.inter : (int64_t)g.n;
+  const i32x4 rB = make_rsrc(g.b + expert * g.b_e, (uint32_t)(b_rows_total * g.b_n));
+  const i32x4 rS = make_rsrc(g.bs + expert * g.bs_e, (uint32_t)(b_rows_total * g.bs_n));
+  const i32x4 rA = make_rsrc(g.a, (uint32_t)(g.a_rows * g.lda * (int64_t)sizeof(T)));
+  const int u0 = wk * U;
+  const int nunits = (g.k + 127) >> 7;
+  const bool s_dword = ((g.bs_n | g.bs_e | (int64_t)reinterpret_cast<uintptr_t>(g.bs)) & 3) == 0;
+  const uint32_t sshift = s_dword ? 8u * grp : 0u;
+
+  // weights and scales of step s into ring slot b (columns past N re-read
+  // row 0; their outputs are not stored)
+  i32x4 braw[2][U][NB];
+  uint32_t sdw[2][NB][U];
+  auto load_step = [&](int s, auto slot_c) {
+    constexpr int b = decltype(slot_c)::value;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int col = col0(s, wn) + c16;
+      const int64_t brow = (nb == 0 ? 0 : g.inter) + (col < g.n ? col : 0);
+      const uint32_t so = (uint32_t)(brow * g.bs_n) + (uint32_t)(u0 * 4);
+      if (s_dword) {
+        if (U == 4) {
+          const i32x4 v = buf_load16(rS, so);
+#pragma unroll
+          for (int uu = 0; uu < U; ++uu) sdw[b][nb][uu] = (uint32_t)v[uu];
+        } else {
+          const i32x2 v = buf_load8(rS, so);
+#pragma unroll
+          for (int uu = 0; uu < U; ++uu) sdw[b][nb][uu] = (uint32_t)v[uu];
+        }
+      } else {
+#pragma unroll
+        for (int uu = 0; uu < U; ++uu) sdw[b][nb][uu] = buf_load_u8(rS, so + 4 * uu + grp);
+      }
+      const uint32_t bo = (uint32_t)(brow * g.b_n);
+#pragma unroll
+      for (int uu = 0; uu < U; ++uu) {
+        const int k0 = (u0 + uu) * 128 + grp * 32;
+        braw[b][uu][nb] = buf_load16(rB, k0 < g.k ? bo + (uint32_t)(k0 >> 1) : kOOB);
+      }
+    }
+  };
+  load_step(0, std::integral_constant<int, 0>{});
+
+  // activation rows: rows 0 .. kStageRows-1 of the block go to LDS with
+  // direct-to-LDS loads, other rows load per lane (as in the skinny kernel)
+  const int64_t arow = (g.sorted_ids || g.route_ids) ? my_route[0] / g.top_k : my_route[0];
+  const uint32_t aoff = my_route[0] >= 0 ? (uint32_t)(arow * g.lda * (int64_t)sizeof(T)) : kOOB;
+  const int a_stride = stage_stride(nunits);
+  {
+    const int qn = (nunits * 256 + 1023) / 1024;
+    for (int i = wave; i < kStageRows * qn; i += WK * WN) {
+      const int br = i / qn, q = i - (i / qn) * qn;
+      const int route = __builtin_amdgcn_readlane((int)my_route[0], br);
+      if (route < 0) continue;
+      const int64_t ar = (g.sorted_ids || g.route_ids) ? route / g.top_k : route;
+      const uint32_t kb = (uint32_t)(q * 1024 + lane * 16);
+      const uint32_t off =
+          kb < (uint32_t)(g.k * (int)sizeof(T)) ? (uint32_t)(ar * g.lda * (int64_t)sizeof(T)) + kb
+                                                : kOOB;
+      llvm_amdgcn_raw_buffer_load_lds(rA, lds_ptr(a_lds + br * a_stride + q * 1024), 16, off, 0, 0,
+                                      0);
+    }
+  }
+  V8 af[U][4];
+#pragma unroll
+  for (int uu = 0; uu < U; ++uu) {
+    const int k0 = (u0 + uu) * 128 + grp * 32;
+    // nothing in this branch consumes the loaded values, so no wait is
+    // placed in it
+    if (k0 < g.k && aoff != kOOB && c16 >= kStageRows) {
+      const uint32_t o = aoff + (uint32_t)(k0 * (int)sizeof(T));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) af[uu][j] = __builtin_bit_cast(V8, buf_load16(rA, o + 16 * j));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) af[uu][j] = zero_v8<V8>();
+    }
+  }
+
+  const float alpha = scalar_alpha(g, expert);
+  static_for<0, CS>([&](auto step_c) {
+    constexpr int s = decltype(step_c)::value;
+    constexpr int b = s & 1;
+    if constexpr (s + 1 < CS) load_step(s + 1, std::integral_constant<int, b ^ 1>{});
+    if constexpr (s == 0) {
+      // the staged rows have landed once at most the next step's loads
+      // (NB scale and U x NB weight loads in the dword-scale path, more
+      // otherwise) are outstanding
+      if constexpr (CS > 1) wait_vmcnt<NB + U * NB>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int uu = 0; uu < U; ++uu) {
+        const bool k_ok = (u0 + uu) * 128 + grp * 32 < g.k;
+        if (c16 < kStageRows && aoff != kOOB && k_ok) {
+          const uint8_t* src = a_lds + c16 * a_stride + (u0 + uu) * 256 + grp * 64;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) af[uu][j] = *reinterpret_cast<const V8*>(src + 16 * j);
+        }
+      }
+    }
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int uu = 0; uu < U; ++uu) {
+      // K past the end: weights read as zero, the scale forced to 1
+      const bool k_ok = (u0 + uu) * 128 + grp * 32 < g.k;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t sb = k_ok ? (sdw[b][nb][uu] >> sshift) & 0xFFu : 127u;
+        const float sc = e8m0_scale(sb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const V8 bf = Decode<T>::run((uint32_t)braw[b][uu][nb][j], sc);
+          acc[nb] = mfma16(af[uu][j], bf, acc[nb]);
+        }
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) red[b][wk][wn][nb][lane] = acc[nb];
+    // publish the partials (a bare barrier: the next step's loads stay in
+    // flight); red[b] is rewritten two steps later, after the next barrier
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    for (int idx = threadIdx.x; idx < WN * 256; idx += WK * WN * 64) {
+      const int w = idx >> 8;
+      const int l = (idx >> 2) & 63;
+      const int i = idx & 3;
+      const int col = col0(s, w) + (l & 15);
+      RowInfo r;
+      r.out_row = srow[(l >> 4) * 4 + i];
+      r.valid = r.out_row >= 0;
+      if (!r.valid || col >= g.n) continue;
+      float v[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        float acc_s = 0.f;
+#pragma unroll
+        for (int q = 0; q < WK; ++q) acc_s += red[b][q][w][nb][l][i];
+        v[nb] = acc_s;
+      }
+      store_out<T, EPI>(g, r, col, alpha, v[0], v[NB - 1]);
+    }
+  });
+}
+
 // ---------------------------------------------------------------- tiled
 template <typename T, int FM, int FN, int EPI>
 __global__ __launch_bounds__(256) void w4a16_tiled(GemmArgs g) {
@@ -642,6 +856,29 @@ void skinny_launch_cg(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStr
   }
 }
 
+template <typename T, int CS, int EPI>
+void stream_launch_cs(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStream_t st) {
+  const int nunits = (g.k + 127) / 128;
+  const size_t lds = (size_t)kStageRows * stage_stride(nunits);
+  switch (s.wk) {
+    case 1: w4a16_stream<T, 1, 4, 4, CS, EPI><<<grid, 256, lds, st>>>(g); break;
+    case 2: w4a16_stream<T, 2, 2, 4, CS, EPI><<<grid, 256, lds, st>>>(g); break;
+    case 4: w4a16_stream<T, 4, 1, 4, CS, EPI><<<grid, 256, lds, st>>>(g); break;
+    default: w4a16_stream<T, 8, 1, 4, CS, EPI><<<grid, 512, lds, st>>>(g); break;
+  }
+}
+
+// Steps per workgroup of the pipelined single-trip kernel: 2 while that
+// keeps >= 512 workgroups (two per CU) busy, else 1 (the skinny kernel).
+// Measured on the MoE decode layer (graph replay, 3 weight copies): M=8
+// 47.4 -> 43.1 us and M=32 97.0 -> 87.5 us with 2 steps; 4 steps (167-172
+// VGPRs, two waves per SIMD) 45.5 / 88.5 us; at M=1 (8 expert blocks) both
+// lose to the skinny kernel.
+int stream_steps(const GemmArgs& g, const SkinnyShape& s, int64_t blocks, int64_t groups) {
+  if (s.rb != 1 || s.cg != 1 || (g.k + 127) / 128 > s.wk * s.u) return 1;
+  return blocks * ((groups + 1) / 2) >= 512 ? 2 : 1;
+}
+
 template <typename T, int RB, int EPI>
 void skinny_launch_rb(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStream_t st) {
   if (s.cg == 2) skinny_launch_cg<T, RB, 2, EPI>(g, s, grid, st);
@@ -691,7 +928,14 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
                                : gy;
     const SkinnyShape sh = skinny_shape(g.k, out_cols, blocks, rb);
     const int tile_cols = 16 * sh.wn * sh.cg;
-    dim3 grid((unsigned)((out_cols + tile_cols - 1) / tile_cols), (unsigned)(gy > 0 ? gy : 1));
+    const int64_t groups = (out_cols + tile_cols - 1) / tile_cols;
+    const int cs = stream_steps(g, sh, blocks, groups);
+    if (cs > 1) {
+      dim3 grid((unsigned)((groups + cs - 1) / cs), (unsigned)(gy > 0 ? gy : 1));
+      stream_launch_cs<T, 2, EPI>(g, sh, grid, st);
+      return launch_status("w4a16 stream launch");
+    }
+    dim3 grid((unsigned)groups, (unsigned)(gy > 0 ? gy : 1));
     if (rb == 1)
       skinny_launch_rb<T, 1, EPI>(g, sh, grid, st);
     else

@@ -159,6 +159,22 @@ def test_linear_fp16_partial_tiles(m):
     assert_parity(y, oracle, ref=ref, what=f"fp16 m={m}")
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_linear_pipelined_decode_grid(dt):
+    # 3 rows over 20480 columns: 640 two-step workgroups take the
+    # software-pipelined decode kernel (dense rows)
+    rng = np.random.default_rng(31)
+    m, k, n = 3, 2048, 20480
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    x = rand_act(31, (m, k), dt)
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    assert y.dtype == dt
+    ref = _safe_reference(cuda(x), packed, scales)
+    oracle = O.linear_fp64(x.float().numpy(), packed, scales,
+                           w_dtype="f16" if dt == torch.float16 else "bf16")
+    assert_parity(y, oracle, ref=ref, what=f"pipelined {dt}")
+
+
 def test_linear_bias_and_leading_dims():
     rng = np.random.default_rng(31)
     n, k = 96, 256

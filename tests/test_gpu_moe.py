@@ -181,6 +181,30 @@ def test_aiter_entry_w4a4_metadata(block_m):
     assert_parity(C.float().cpu().numpy(), oracle)
 
 
+def test_aiter_entry_pipelined_decode_grid():
+    # 16-row blocks over enough expert blocks x column groups (>= 512
+    # two-step workgroups) take the software-pipelined decode kernel; one
+    # expert's blocks are marked not on this device (-1)
+    rng = np.random.default_rng(77)
+    m, k, n, e, top_k, block_m = 48, 512, 8192, 16, 4, 16
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(77, (m, k))
+    w, ids = _route(m, e, top_k, 177)
+    srt, exp_, npp = O.make_routing(ids.numpy(), block_m=block_m, num_experts=e)
+    exp_ = exp_.copy()
+    exp_[exp_ == 3] = -1
+    C = torch.full((m, top_k, n), 3.0, dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4(cuda(a), cuda(wp), C, torch.tensor([0.5], device="cuda"),
+                       torch.linspace(1, 2, e, device="cuda"), None, cuda(ws), cuda(w), cuda(ids),
+                       cuda(srt), cuda(exp_), cuda(npp), True, top_k, False, False,
+                       {"BLOCK_SIZE_M": block_m}, torch.bfloat16)
+    ids_np = ids.numpy()
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 0.5, np.linspace(1, 2, e), w.numpy(),
+                              ids_np, True)
+    oracle[ids_np == 3] = 0.0
+    assert_parity(C.float().cpu().numpy(), oracle)
+
+
 # ---------------------------------------------------------------- routing
 
 @pytest.mark.parametrize("n_tokens,top_k,num_experts,block_m",
