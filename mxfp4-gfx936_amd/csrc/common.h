@@ -99,6 +99,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// s_barrier without __syncthreads' release / acquire fences (which would
+// wait for every outstanding global load).  The empty asm statements with
+// memory clobbers keep the compiler from moving memory accesses across it;
+// callers wait for the LDS traffic the barrier publishes themselves.
+__device__ __forceinline__ void barrier_only() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ lds_u32* lds_ptr(uint8_t* p) {
   return (lds_u32*)(__attribute__((address_space(3))) uint8_t*)p;
 }

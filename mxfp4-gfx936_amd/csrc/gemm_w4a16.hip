@@ -328,7 +328,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
       if (stage) {
         // the staged rows have landed once every wave's loads are done
         wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
+        barrier_only();
 #pragma unroll
         for (int uu = 0; uu < U; ++uu)
 #pragma unroll
@@ -555,7 +555,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_stream(GemmArgs g) {
       // otherwise) are outstanding
       if constexpr (CS > 1) wait_vmcnt<NB + U * NB>();
       else wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();
+      barrier_only();
 #pragma unroll
       for (int uu = 0; uu < U; ++uu) {
         const bool k_ok = (u0 + uu) * 128 + grp * 32 < g.k;

@@ -205,7 +205,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
     if (STAGES >= 4 && later >= 2) wait_vmcnt<2 * PER_STAGE>();
     else if (STAGES >= 3 && later >= 1) wait_vmcnt<PER_STAGE>();
     else wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
+    barrier_only();
     if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
     const uint8_t* base = smem + (kt % STAGES) * S::STAGE;
     const uint8_t* As = base;
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
 
   // ---- epilogue: lane owns row wm*FM*16 + fm*16 + c16 and columns
   // wn*FN*16 + fn*16 + grp*4 .. +3; stage rows in LDS, write 16-byte chunks
-  __builtin_amdgcn_s_barrier();  // every wave is done reading the stage buffers
+  barrier_only();  // every wave is done reading the stage buffers
   const float alpha = scalar_alpha(g, expert);
 #pragma unroll
   for (int pass = 0; pass < EPI_PASSES; ++pass) {
