@@ -890,16 +890,24 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
   const int64_t cap = g.m;  // dense rows or sorted capacity
   const bool routed = g.sorted_ids != nullptr;
   const int out_cols = g.n;
-  // skinny for 16/32-row blocks (and any routed block size that is not a
-  // multiple of 32); tiled otherwise.
+  // skinny for 16-row routed blocks (and any routed block size that is not
+  // a multiple of 32) and dense M <= 32; tiled otherwise.  Routed 32-row
+  // blocks take the 32 x 128 prefill tile: the 32-row skinny kernel loads
+  // each block's activation rows per wave (MoE layer, 32-row blocks, 512
+  // tokens: 415 vs 144 us).  Dense M <= 128 also takes 32-row skinny blocks
+  // when the prefill grid would be small and its K loop long (fewer than
+  // 128 workgroups, >= 48 stages of 64): o_proj K=4096 N=2048 at M=33-128
+  // runs 12-20 us that way against ~25 us.
   int skinny_rb = 0;
   if (g.route_ids) {
     skinny_rb = 1;  // direct routing: one workgroup row per route
   } else if (routed) {
     if (g.block_m % 32 != 0) skinny_rb = 1;
-    else if (g.block_m == 32) skinny_rb = 2;
   } else if (cap <= 32) {
     skinny_rb = cap <= 16 ? 1 : 2;
+  } else if (cap <= 128) {
+    const int64_t pf_wgs = ((cap + 31) / 32) * ((out_cols + 127) / 128);
+    if (pf_wgs < 128 && g.k / 64 >= 48) skinny_rb = 2;
   }
   // the skinny kernel addresses its operands through 2 GiB buffer
   // resources; larger operands go to the tiled kernel where the block size

@@ -47,9 +47,9 @@ def _backend() -> str:
 def _routing_block_m(num_routes: int, num_experts: int) -> int:
     """Rows per expert block for the routed GEMMs, from the mean rows per expert."""
     avg = num_routes / max(num_experts, 1)
-    if avg <= 8:
+    if avg <= 10:
         return 16
-    if avg <= 20:
+    if avg <= 24:
         return 32
     if avg <= 80:
         return 64

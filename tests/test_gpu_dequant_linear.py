@@ -159,6 +159,20 @@ def test_linear_fp16_partial_tiles(m):
     assert_parity(y, oracle, ref=ref, what=f"fp16 m={m}")
 
 
+@pytest.mark.parametrize("m", [33, 96, 128])
+def test_linear_mid_m_long_k(m):
+    # o_proj shape, 33 <= M <= 128: 32-row skinny blocks (the prefill grid
+    # would be under 128 workgroups with a 64-stage K loop)
+    rng = np.random.default_rng(400 + m)
+    k, n = 4096, 2048
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    x = rand_act(400 + m, (m, k))
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    ref = _safe_reference(cuda(x), packed, scales)
+    oracle = O.linear_fp64(x.float().numpy(), packed, scales)
+    assert_parity(y, oracle, ref=ref, what=f"mid m={m}")
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_linear_pipelined_decode_grid(dt):
     # 3 rows over 20480 columns: 640 two-step workgroups take the

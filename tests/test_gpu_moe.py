@@ -239,7 +239,7 @@ def layer_weights():
     return _layer_weights(20260815)
 
 
-@pytest.mark.parametrize("m", [1, 8, 32, 512, 4096])
+@pytest.mark.parametrize("m", [1, 8, 32, 256, 512, 4096])
 def test_moe_layer_vs_oracle(m, layer_weights):
     w13, s13, w2, s2 = layer_weights
     x = rand_act(20260816 + m, (m, 2048))
