@@ -11,6 +11,7 @@
 // bf16/fp16, for all 16 codes x 256 scales.
 #pragma once
 
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -97,6 +98,16 @@ extern "C" __device__ void llvm_amdgcn_raw_buffer_load_lds(i32x4 rsrc, lds_u32* 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Calls f(std::integral_constant<int, I>{}) for I = B .. E-1 (compile-time
+// indices for register arrays and template arguments inside loops).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 // s_barrier without __syncthreads' release / acquire fences (which would

@@ -409,14 +409,6 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
 // once per CS column groups, and keeps weight loads streaming through the
 // epilogues.  Same loads, rounding and reduction order as the skinny
 // kernel, so results are identical.
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 template <typename T, int WK, int WN, int U, int CS, int EPI>
 __global__ __launch_bounds__(WK * WN * 64) void w4a16_stream(GemmArgs g) {
   typedef typename V8Of<T>::type V8;

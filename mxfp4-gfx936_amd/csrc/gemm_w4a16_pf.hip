@@ -91,7 +91,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   constexpr int SMEM = S::PIPE > EPI_ROWS * C_LD ? S::PIPE : EPI_ROWS * C_LD;
   static_assert(BN % 32 == 0 && EPI_ROWS % 16 == 0, "tile config");
   static_assert(STAGES == 2 || S::EVEN, "multi-stage waits count loads per wave");
-  static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 stages");
+  static_assert(STAGES >= 2 && STAGES <= 8, "2 to 8 stages");
+  static_assert((STAGES - 2) * (S::A_PER + S::B_PER) <= 63, "vmcnt holds at most 63");
   static_assert(EPI != EPI_SILU_MUL || FN % 2 == 0, "SiLU pairs need even FN");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
   uint8_t* const sA = smem;
@@ -229,9 +230,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     // one scale load on even stages, which waiting for PER_STAGE covers)
     constexpr int PER_STAGE = S::A_PER + S::B_PER;
     const int later = (nk - 1 - kt) < (STAGES - 2) ? (nk - 1 - kt) : (STAGES - 2);
-    if (STAGES >= 4 && later >= 2) wait_vmcnt<2 * PER_STAGE>();
-    else if (STAGES >= 3 && later >= 1) wait_vmcnt<PER_STAGE>();
-    else wait_vmcnt<0>();
+    static_for<0, STAGES - 1>([&](auto c) {
+      if (later == decltype(c)::value) wait_vmcnt<decltype(c)::value * PER_STAGE>();
+    });
     barrier_only();
     if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
     const uint8_t* As = sA + (kt % STAGES) * S::A_STAGE;
@@ -389,6 +390,7 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 // 256, 64 x 256/512, 32 x 256/512; 5 or 10 waves (a wave count that is not
 // a multiple of the 4 SIMDs loads one SIMD twice); 3-4 stages at 128 rows
 // (the extra LDS costs a workgroup per CU: -10-20% for the routed GEMMs);
+// 4-8 stages at 32 x 128 and 5 at 64 x 128 (M = 256-1024: 0-15% slower);
 // weights prefetched 2-4 stages ahead of the activations (no gain: the
 // routed GEMMs wait on activation rows as much).
 template <typename T, int EPI>
