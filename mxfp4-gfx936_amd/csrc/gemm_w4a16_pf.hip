@@ -101,7 +101,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave index as a scalar: the per-wave load choices and LDS addresses
+  // (M0) then need no lane-to-scalar moves or exec masking
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
   const int c16 = lane & 15;
   const int grp = lane >> 4;
