@@ -173,7 +173,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // staged activation rows
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
   const int wk = wave % WK;
   const int wn = wave / WK;
   const int c16 = lane & 15;
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_stream(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t a_lds[];  // staged activation rows
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
   const int wk = wave % WK;
   const int wn = wave / WK;
   const int c16 = lane & 15;

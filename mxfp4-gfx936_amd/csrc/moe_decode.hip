@@ -50,7 +50,7 @@ __global__ __launch_bounds__(RW * WK * 64) void moe_down_topk(DownArgs a) {
   __shared__ f32x4 red[WK][64];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
   const int wk = wave % WK;
   const int rw = wave / WK;
   const int c16 = lane & 15;
