@@ -22,10 +22,13 @@ namespace mx {
 namespace {
 
 constexpr int kChunk = 1024;  // routes per count/place workgroup
-// Routes the single-workgroup routing handles: at 1024 it replaces three
-// launches with one 7 us kernel; at 4096 its serial 256-route passes took
-// 24 us against 16 us for the three-launch path.
+// Routes the single-workgroup routing handles: up to kSingle one 256-thread
+// workgroup (7-8 us instead of three launches); up to kSingleWide one
+// 1024-thread workgroup (four 1024-route placement chunks; 4096 routes:
+// 12.2 us against 15.4 us of kernel time for the three launches, MoE layer
+// at 512 tokens 132.7 -> 128.9 us, at 256 tokens 114.6 -> 108.9 us).
 constexpr int kSingle = 1024;
+constexpr int kSingleWide = 4096;
 // Layers with at most this many routes use direct routing in the GEMMs
 // (no kernel builds sorted metadata); must not exceed the skinny kernel's
 // scan limit (256).
@@ -222,39 +225,45 @@ __global__ __launch_bounds__(256) void topk_sum(const T* __restrict__ d, const T
   }
 }
 
-// All three passes in one workgroup for at most kSingle routes (decode and
-// small prefill): the histogram, the padded exclusive scan over experts
-// (each thread owns kMaxExperts / 256 consecutive experts), and the ballot
-// placement of align_place, separated by barriers instead of launches.
-template <typename TI>
-__global__ __launch_bounds__(256) void align_single(const TI* __restrict__ ids, int64_t n,
-                                                    int num_experts, int id_bits, int block_m,
-                                                    int32_t* __restrict__ sorted_ids,
-                                                    int32_t* __restrict__ expert_ids,
-                                                    int32_t* __restrict__ num_post_padded) {
-  constexpr int EPT = kMaxExperts / 256;  // experts per thread in the scan
+// All three passes in one workgroup of NT threads for at most NT * RPT
+// routes (decode and small prefill): the histogram, the padded exclusive
+// scan over experts (each thread owns kMaxExperts / NT consecutive
+// experts), and the ballot placement of align_place over chunks of NT
+// routes, separated by barriers instead of launches.
+template <typename TI, int NT, int RPT>
+__global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, int64_t n,
+                                                   int num_experts, int id_bits, int block_m,
+                                                   int32_t* __restrict__ sorted_ids,
+                                                   int32_t* __restrict__ expert_ids,
+                                                   int32_t* __restrict__ num_post_padded) {
+  constexpr int W = NT / 64;              // waves
+  constexpr int EPT = kMaxExperts / NT;   // experts per thread in the scan
   __shared__ int cursor[kMaxExperts];     // counts, then start positions
-  __shared__ int wcnt[4][kMaxExperts];
-  __shared__ int part[256];
+  __shared__ int wcnt[W][kMaxExperts];
+  __shared__ int part[W];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  for (int e = tid; e < kMaxExperts; e += 256) {
+  for (int e = tid; e < kMaxExperts; e += NT) {
     cursor[e] = 0;
-    wcnt[0][e] = wcnt[1][e] = wcnt[2][e] = wcnt[3][e] = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) wcnt[w][e] = 0;
   }
   __syncthreads();
-  int eid[kSingle / 256];
+  int eid[RPT];
 #pragma unroll
-  for (int it = 0; it < kSingle / 256; ++it) {
-    const int64_t r = it * 256 + tid;
+  for (int it = 0; it < RPT; ++it) {
+    const int64_t r = it * NT + tid;
     int64_t e64 = -1;
     if (r < n) e64 = (int64_t)ids[r];
     eid[it] = (e64 >= 0 && e64 < num_experts) ? (int)e64 : -1;
-    if (eid[it] >= 0) atomicAdd(&cursor[eid[it]], 1);
   }
+#pragma unroll
+  for (int it = 0; it < RPT; ++it)
+    if (eid[it] >= 0) atomicAdd(&cursor[eid[it]], 1);
   __syncthreads();
-  // padded exclusive scan: thread tid owns experts tid*EPT .. +EPT
+  // padded exclusive scan: thread tid owns experts tid*EPT .. +EPT; the
+  // per-thread totals are scanned with wave shuffles, then the wave sums
   int cnt[EPT], pad[EPT], local = 0;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
@@ -263,15 +272,16 @@ __global__ __launch_bounds__(256) void align_single(const TI* __restrict__ ids, 
     pad[j] = (cnt[j] + block_m - 1) / block_m * block_m;
     local += pad[j];
   }
-  part[tid] = local;
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
-    const int v = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
+  int v = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off);
+    if (lane >= off) v += u;
   }
-  int start = part[tid] - local;
+  if (lane == 63) part[wave] = v;
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) v += part[w];
+  int start = v - local;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
     const int e = tid * EPT + j;
@@ -282,13 +292,13 @@ __global__ __launch_bounds__(256) void align_single(const TI* __restrict__ ids, 
     }
     start += pad[j];
   }
-  if (tid == 255) num_post_padded[0] = part[255];
+  if (tid == NT - 1) num_post_padded[0] = v;
   __syncthreads();
   // placement in route order (align_place with this workgroup's cursors)
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
-  for (int it = 0; it < kSingle / 256; ++it) {
-    const int64_t r = it * 256 + tid;
+  for (int it = 0; it < RPT; ++it) {
+    const int64_t r = it * NT + tid;
     const bool valid = eid[it] >= 0;
     const int e = valid ? eid[it] : 0;
     uint64_t same = __ballot(valid);
@@ -306,9 +316,14 @@ __global__ __launch_bounds__(256) void align_single(const TI* __restrict__ ids, 
       sorted_ids[before] = (int32_t)r;
     }
     __syncthreads();
-    for (int x = tid; x < num_experts; x += 256) {
-      cursor[x] += wcnt[0][x] + wcnt[1][x] + wcnt[2][x] + wcnt[3][x];
-      wcnt[0][x] = wcnt[1][x] = wcnt[2][x] = wcnt[3][x] = 0;
+    for (int x = tid; x < num_experts; x += NT) {
+      int add = 0;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        add += wcnt[w][x];
+        wcnt[w][x] = 0;
+      }
+      cursor[x] += add;
     }
     __syncthreads();
   }
@@ -346,8 +361,13 @@ int launch_align(const TI* ids, int64_t n, int num_experts, int block_m, int32_t
   int id_bits = 0;
   while ((1 << id_bits) < num_experts) ++id_bits;
   if (n <= kSingle) {
-    align_single<TI><<<1, 256, 0, st>>>(ids, n, num_experts, id_bits, block_m, sorted_ids,
-                                        expert_ids, npp);
+    align_single<TI, 256, kSingle / 256><<<1, 256, 0, st>>>(ids, n, num_experts, id_bits, block_m,
+                                                            sorted_ids, expert_ids, npp);
+    return launch_status("align launch");
+  }
+  if (n <= kSingleWide) {
+    align_single<TI, 1024, kSingleWide / 1024><<<1, 1024, 0, st>>>(
+        ids, n, num_experts, id_bits, block_m, sorted_ids, expert_ids, npp);
     return launch_status("align launch");
   }
   if (nchunks > 0) {
