@@ -227,6 +227,44 @@ def decode_probe() -> int:
     return 0
 
 
+def data_probe() -> int:
+    """Steady-clock time of the headline GEMM on random inputs (the bench's)
+    and on all-zero / constant ones.  The kernel and the work are the same;
+    only the data differs, so a gap is the chip's power management lowering
+    the clock while random operands keep the MFMAs switching."""
+    import numpy as np
+    import torch
+
+    import mxfp4_amd as mx
+    mx._lib.load()
+    m, k, n = 4096, 2048, 5120
+    rng = np.random.default_rng(20260810 + 1)
+    (w, s), = rand_weights(rng, (n,), k)
+    x = randn_bf16(20260810, (m, k))
+    cases = {
+        "random": (x, w),
+        "zeros": (torch.zeros_like(x), torch.zeros_like(w)),
+        "x_zero": (torch.zeros_like(x), w),
+        "codes_zero": (x, torch.zeros_like(w)),
+        "constant": (torch.full_like(x, 1.5), torch.full_like(w, 0x22)),
+    }
+    res = {}
+    for name, (xa, wa) in cases.items():
+        ramp_clocks(lambda: mx.linear_mxfp4_soft(xa, wa, s))
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(300):
+            mx.linear_mxfp4_soft(xa, wa, s)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / 300 * 1e3
+        res[name] = {"us": round(us, 2), "tflops": round(2.0 * m * n * k / us / 1e6, 1)}
+        log(f"data probe {name}: {us:.2f} us")
+    print(json.dumps({"probe": "data", "m": m, "k": k, "n": n, "results": res}))
+    return 0
+
+
 def linear_bytes(m, n, k):
     return n * k // 2 + n * k // 32 + 2 * m * k + 2 * m * n
 
@@ -368,6 +406,8 @@ def main() -> int:
                     help="only run the launches the counter runs measure")
     ap.add_argument("--decode-probe", action="store_true",
                     help="only run decode launches for counter / trace runs")
+    ap.add_argument("--data-probe", action="store_true",
+                    help="time the headline GEMM on random vs zero / constant inputs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -378,6 +418,8 @@ def main() -> int:
         return traffic_probe()
     if args.decode_probe:
         return decode_probe()
+    if args.data_probe:
+        return data_probe()
 
     import numpy as np
     import torch

@@ -39,13 +39,6 @@ int launch_status(const char* what);             // checks hipGetLastError()
 
 // ---------------------------------------------------------------- device side
 
-// E8M0 byte -> scale operand of v_cvt_scalef32_pk_*_fp4.  The converter
-// reads only the exponent field of that operand (verified on the device for
-// every scale byte x every code pair: a mantissa of 0.5 changes no output
-// bit), so the byte goes straight into the exponent.  The 0x400000 mantissa
-// bit makes s = 0 the subnormal 2^-127 and s = 255 a quiet NaN, the two
-// encodings the converter is known to treat as 2^-127 and NaN.  One
-// v_lshl_or_b32.  The result is only meaningful as the converter's operand.
 // Raw (MUBUF) buffer loads through a 128-bit resource {base, byte size,
 // raw-buffer flags}: a lane whose byte offset lies at or past the size reads
 // zero instead of memory.  Kernels use kOOB for padding rows and K tails,
@@ -124,6 +117,13 @@ __device__ __forceinline__ lds_u32* lds_ptr(uint8_t* p) {
   return (lds_u32*)(__attribute__((address_space(3))) uint8_t*)p;
 }
 
+// E8M0 byte -> scale operand of v_cvt_scalef32_pk_*_fp4.  The converter
+// reads only the exponent field of that operand (verified on the device for
+// every scale byte x every code pair: a mantissa of 0.5 changes no output
+// bit), so the byte goes straight into the exponent.  The 0x400000 mantissa
+// bit makes s = 0 the subnormal 2^-127 and s = 255 a quiet NaN, the two
+// encodings the converter is known to treat as 2^-127 and NaN.  One
+// v_lshl_or_b32.  The result is only meaningful as the converter's operand.
 __device__ __forceinline__ float e8m0_scale(uint32_t s) {
   return __uint_as_float((s << 23) | 0x00400000u);
 }
