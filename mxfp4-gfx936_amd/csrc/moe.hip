@@ -23,10 +23,9 @@ namespace {
 
 constexpr int kChunk = 1024;  // routes per count/place workgroup
 // Routes the single-workgroup routing handles: up to kSingle one 256-thread
-// workgroup (7-8 us instead of three launches); up to kSingleWide one
-// 1024-thread workgroup (four 1024-route placement chunks; 4096 routes:
-// 12.2 us against 15.4 us of kernel time for the three launches, MoE layer
-// at 512 tokens 132.7 -> 128.9 us, at 256 tokens 114.6 -> 108.9 us).
+// workgroup (256 routes: 4.9 us); up to kSingleWide one 1024-thread
+// workgroup (1024-route placement chunks; 2048 routes: 6.6 us, 4096: 10.0
+// us, against 15.4 us of kernel time for the three launches).
 constexpr int kSingle = 1024;
 constexpr int kSingleWide = 4096;
 // Layers with at most this many routes use direct routing in the GEMMs
@@ -34,6 +33,9 @@ constexpr int kSingleWide = 4096;
 // scan limit (256).
 constexpr int64_t kDirectRoutes = 64;
 constexpr int kMaxExperts = 1024;
+// Experts the single-workgroup routing kernel holds in LDS (more use the
+// three-launch path).
+constexpr int kSingleExperts = 256;
 
 template <typename TI>
 __global__ __launch_bounds__(256) void align_count(const TI* __restrict__ ids, int64_t n,
@@ -226,29 +228,33 @@ __global__ __launch_bounds__(256) void topk_sum(const T* __restrict__ d, const T
 }
 
 // All three passes in one workgroup of NT threads for at most NT * RPT
-// routes (decode and small prefill): the histogram, the padded exclusive
-// scan over experts (each thread owns kMaxExperts / NT consecutive
-// experts), and the ballot placement of align_place over chunks of NT
-// routes, separated by barriers instead of launches.
+// routes and kSingleExperts experts (decode and small prefill): the
+// histogram, the padded exclusive scan over experts (each thread owns EPT
+// consecutive experts), and the ballot placement of align_place over chunks
+// of NT routes, separated by barriers instead of launches.  Placement of a
+// chunk: each wave counts its routes per expert (ballots), one pass over
+// the experts turns the counts into each wave's first position (after the
+// earlier chunks and the lower waves), and every route lands at its wave's
+// position + its rank among the lower lanes -- route order within an
+// expert, as align_place.  The counts are double-buffered by chunk parity,
+// so a chunk costs two barriers; chunks past the last route are skipped.
 template <typename TI, int NT, int RPT>
 __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, int64_t n,
                                                    int num_experts, int id_bits, int block_m,
                                                    int32_t* __restrict__ sorted_ids,
                                                    int32_t* __restrict__ expert_ids,
                                                    int32_t* __restrict__ num_post_padded) {
-  constexpr int W = NT / 64;              // waves
-  constexpr int EPT = kMaxExperts / NT;   // experts per thread in the scan
-  __shared__ int cursor[kMaxExperts];     // counts, then start positions
-  __shared__ int wcnt[W][kMaxExperts];
+  constexpr int W = NT / 64;                              // waves
+  constexpr int E = kSingleExperts;
+  constexpr int EPT = (E + NT - 1) / NT;                  // experts per thread in the scan
+  __shared__ int cursor[2][E];    // counts, then each expert's next position (by chunk parity)
+  __shared__ int wbase[2][W][E];  // per-wave counts, then per-wave first positions
   __shared__ int part[W];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  for (int e = tid; e < kMaxExperts; e += NT) {
-    cursor[e] = 0;
-#pragma unroll
-    for (int w = 0; w < W; ++w) wcnt[w][e] = 0;
-  }
+  for (int i = tid; i < 2 * E; i += NT) (&cursor[0][0])[i] = 0;
+  for (int i = tid; i < 2 * W * E; i += NT) (&wbase[0][0][0])[i] = 0;
   __syncthreads();
   int eid[RPT];
 #pragma unroll
@@ -260,7 +266,7 @@ __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, i
   }
 #pragma unroll
   for (int it = 0; it < RPT; ++it)
-    if (eid[it] >= 0) atomicAdd(&cursor[eid[it]], 1);
+    if (eid[it] >= 0) atomicAdd(&cursor[0][eid[it]], 1);
   __syncthreads();
   // padded exclusive scan: thread tid owns experts tid*EPT .. +EPT; the
   // per-thread totals are scanned with wave shuffles, then the wave sums
@@ -268,7 +274,7 @@ __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, i
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
     const int e = tid * EPT + j;
-    cnt[j] = e < num_experts ? cursor[e] : 0;
+    cnt[j] = e < num_experts ? cursor[0][e] : 0;
     pad[j] = (cnt[j] + block_m - 1) / block_m * block_m;
     local += pad[j];
   }
@@ -286,7 +292,7 @@ __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, i
   for (int j = 0; j < EPT; ++j) {
     const int e = tid * EPT + j;
     if (e < num_experts) {
-      cursor[e] = start;
+      cursor[0][e] = start;
       for (int blk = start / block_m; blk < (start + pad[j]) / block_m; ++blk) expert_ids[blk] = e;
       for (int p = start + cnt[j]; p < start + pad[j]; ++p) sorted_ids[p] = (int32_t)n;
     }
@@ -294,10 +300,11 @@ __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, i
   }
   if (tid == NT - 1) num_post_padded[0] = v;
   __syncthreads();
-  // placement in route order (align_place with this workgroup's cursors)
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
   for (int it = 0; it < RPT; ++it) {
+    if ((int64_t)it * NT >= n) break;  // the same for every thread
+    const int pb = it & 1;
     const int64_t r = it * NT + tid;
     const bool valid = eid[it] >= 0;
     const int e = valid ? eid[it] : 0;
@@ -308,24 +315,23 @@ __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, i
       same &= b ? bal : ~bal;
     }
     const int rank = __popcll(same & lt_mask);
-    if (valid && rank == 0) wcnt[wave][e] = __popcll(same);
-    __syncthreads();
-    if (valid) {
-      int before = cursor[e] + rank;
-      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
-      sorted_ids[before] = (int32_t)r;
-    }
+    if (valid && rank == 0) wbase[pb][wave][e] = __popcll(same);
     __syncthreads();
     for (int x = tid; x < num_experts; x += NT) {
-      int add = 0;
+      int c[W];  // all reads first: one LDS round trip, not W
+#pragma unroll
+      for (int w = 0; w < W; ++w) c[w] = wbase[pb][w][x];
+      int pos = cursor[pb][x];
 #pragma unroll
       for (int w = 0; w < W; ++w) {
-        add += wcnt[w][x];
-        wcnt[w][x] = 0;
+        wbase[pb][w][x] = pos;
+        wbase[pb ^ 1][w][x] = 0;  // the next chunk's counts
+        pos += c[w];
       }
-      cursor[x] += add;
+      cursor[pb ^ 1][x] = pos;
     }
     __syncthreads();
+    if (valid) sorted_ids[wbase[pb][wave][e] + rank] = (int32_t)r;
   }
 }
 
@@ -360,12 +366,13 @@ int launch_align(const TI* ids, int64_t n, int num_experts, int block_m, int32_t
                  hipStream_t st) {
   int id_bits = 0;
   while ((1 << id_bits) < num_experts) ++id_bits;
-  if (n <= kSingle) {
+  const bool single = num_experts <= kSingleExperts;
+  if (single && n <= kSingle) {
     align_single<TI, 256, kSingle / 256><<<1, 256, 0, st>>>(ids, n, num_experts, id_bits, block_m,
                                                             sorted_ids, expert_ids, npp);
     return launch_status("align launch");
   }
-  if (n <= kSingleWide) {
+  if (single && n <= kSingleWide) {
     align_single<TI, 1024, kSingleWide / 1024><<<1, 1024, 0, st>>>(
         ids, n, num_experts, id_bits, block_m, sorted_ids, expert_ids, npp);
     return launch_status("align launch");

@@ -208,8 +208,9 @@ def test_aiter_entry_pipelined_decode_grid():
 # ---------------------------------------------------------------- routing
 
 @pytest.mark.parametrize("n_tokens,top_k,num_experts,block_m",
-                         [(1, 8, 128, 16), (8, 8, 128, 16), (33, 4, 16, 32), (512, 8, 128, 64),
-                          (700, 3, 7, 128), (4096, 8, 128, 128)])
+                         [(1, 8, 128, 16), (8, 8, 128, 16), (33, 4, 16, 32), (128, 8, 128, 32),
+                          (100, 8, 256, 16), (256, 8, 128, 64), (512, 8, 128, 64),
+                          (700, 3, 7, 128), (64, 4, 300, 16), (4096, 8, 128, 128)])
 def test_device_routing_matches_oracle(n_tokens, top_k, num_experts, block_m):
     g = torch.Generator().manual_seed(n_tokens * 7 + top_k)
     ids = torch.randint(-1, num_experts + 1, (n_tokens, top_k), generator=g)
