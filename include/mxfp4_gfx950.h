@@ -91,6 +91,20 @@ int mxfp4_linear_w4a16(const void* x, int x_dtype, int64_t m, int64_t k, int64_t
                        void* out, void* stream);
 
 /*
+ * The same operation (soft:310-376) with a caller-provided device workspace
+ * of at least the bytes mxfp4_linear_w4a16_workspace_size(m, k, n, &bytes)
+ * reports, 16-byte aligned.  A non-zero size means the GEMM is too small to
+ * fill the GPU: K is then split into slices whose FP32 partial sums go
+ * through the workspace and are added in a fixed order (deterministic, but
+ * not bitwise equal to the unsplit sum).  workspace may be NULL (no split).
+ */
+int mxfp4_linear_w4a16_workspace_size(int64_t m, int64_t k, int64_t n, int64_t* bytes);
+int mxfp4_linear_w4a16_ws(const void* x, int x_dtype, int64_t m, int64_t k, int64_t x_row_stride,
+                          const uint8_t* packed, const uint8_t* scales, int64_t n,
+                          const void* bias, void* out, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/*
  * Dense W4A4: both operands packed MXFP4, on gfx950's block-scaled MFMA
  * (the packed-A semantics of aiter:206-214, 329-338 with one expert).
  * a u8 [m, k/2], a_mx u8 [m, k/32], b u8 [n, k/2], b_mx u8 [n, k/32] (all

@@ -16,6 +16,7 @@ namespace mx {
 enum Epilogue {
   EPI_STORE = 0,     // c = T(acc * alpha [* route_w] [+ bias])
   EPI_SILU_MUL = 1,  // gate/up column pairs -> h = silu(g) * u, rounded like vllm:249-252
+  EPI_PARTIAL = 2,   // FP32 partial sums of one K slice (split K, dense only)
 };
 
 struct GemmArgs {
@@ -51,6 +52,10 @@ struct GemmArgs {
   // its expert, together with the next 15 routes of that expert.
   const void* route_ids;
   int32_t ids64;
+  // Split K (dense, plain epilogue): `splitk` K slices, slice s written as
+  // FP32 to splitk_ws + s * m * n, then summed by splitk_reduce.
+  float* splitk_ws;
+  int32_t splitk;
 };
 
 // Per-row routing lookup used by every kernel.
@@ -101,8 +106,8 @@ __device__ __forceinline__ int64_t rows_in_use(const GemmArgs& g) {
 // weights are fetched into few L2s, and every XCD gets an equal share of
 // the live rows.  Returns false for workgroups past the live range.
 __device__ __forceinline__ bool tile_of(const GemmArgs& g, int bm_rows, int nbm, int nbn, int& bm,
-                                        int& bn) {
-  const int x = blockIdx.x % 8, i = blockIdx.x / 8;
+                                        int& bn, int idx, int nwg) {
+  const int x = idx % 8, i = idx / 8;
   if (g.sorted_ids) {
     const int live = (int)((rows_in_use(g) + bm_rows - 1) / bm_rows);
     const int lo = (int)((int64_t)live * x / 8), hi = (int)((int64_t)live * (x + 1) / 8);
@@ -110,7 +115,7 @@ __device__ __forceinline__ bool tile_of(const GemmArgs& g, int bm_rows, int nbm,
     bn = i % nbn;
     return bm < hi;
   }
-  const int nwg = gridDim.x, per = nwg / 8, rem = nwg % 8;
+  const int per = nwg / 8, rem = nwg % 8;
   const int pid = x * per + (x < rem ? x : rem) + i;
   constexpr int GROUP = 4;
   const int first_m = (pid / (GROUP * nbn)) * GROUP;
@@ -139,6 +144,18 @@ enum PfConfig {
 bool pf_supported(const GemmArgs& g, int elem_bytes);
 int pf_choose(const GemmArgs& g, int epi);
 int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t st);
+// Split-K plan for a dense plain-epilogue GEMM whose tiles would not fill
+// the chip: the tile configuration and slice count (1 = no split).
+struct SplitPlan {
+  int cfg, splits;
+};
+SplitPlan splitk_plan(int64_t m, int64_t k, int64_t n);
+// Rows per skinny block (1 or 2 x 16) the dense W4A16 GEMM of these sizes
+// runs with, 0 for the prefill kernels; split_ok: a split-K workspace is given.
+int dense_skinny_rows(int64_t m, int64_t k, int64_t n, bool split_ok);
+int64_t splitk_ws_bytes(int64_t m, int64_t k, int64_t n);
+// Sums the FP32 slices, adds the bias and rounds to T (dtype) into g.c.
+int launch_splitk_reduce(const GemmArgs& g, int dtype, hipStream_t st);
 int launch_w4a4(const GemmArgs& g, int out_dtype, hipStream_t st);
 // Direct-to-LDS W4A4 kernel (gemm_w4a4_pf.hip).
 enum P4Config {

@@ -877,13 +877,31 @@ void skinny_launch_rb(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStr
   else skinny_launch_cg<T, RB, 1, EPI>(g, s, grid, st);
 }
 
+}  // namespace
+
+int dense_skinny_rows(int64_t m, int64_t k, int64_t n, bool split_ok) {
+  if (m <= 16) return 1;
+  if (m <= 32) return 2;
+  if (m > 128) return 0;
+  const int64_t pf_wgs = ((m + 31) / 32) * ((n + 127) / 128);
+  if (pf_wgs >= 128 || k / 64 < 48) return 0;
+  // given a split-K workspace, M > 64 or K > 4096 run faster as split-K
+  // prefill tiles (o_proj M=96 / 128: 19.6 -> 13.7 / 14.9 us; K=8192
+  // N=1024 M=64: 19.5 -> 13.7 us; o_proj M <= 64 stays at ~11.2 us skinny)
+  if (split_ok && (m > 64 || k > 4096) && splitk_plan(m, k, n).splits > 1) return 0;
+  return 2;
+}
+
+namespace {
+
 template <typename T, int EPI>
 int launch_typed(const GemmArgs& g, hipStream_t st) {
   const int64_t cap = g.m;  // dense rows or sorted capacity
   const bool routed = g.sorted_ids != nullptr;
   const int out_cols = g.n;
   // skinny for 16-row routed blocks (and any routed block size that is not
-  // a multiple of 32) and dense M <= 32; tiled otherwise.  Routed 32-row
+  // a multiple of 32) and dense M <= 32; tiled otherwise (split K for
+  // dense grids too small to fill the GPU, when a workspace is given).  Routed 32-row
   // blocks take the 32 x 128 prefill tile: the 32-row skinny kernel loads
   // each block's activation rows per wave (MoE layer, 32-row blocks, 512
   // tokens: 415 vs 144 us).  Dense M <= 128 also takes 32-row skinny blocks
@@ -895,11 +913,8 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
     skinny_rb = 1;  // direct routing: one workgroup row per route
   } else if (routed) {
     if (g.block_m % 32 != 0) skinny_rb = 1;
-  } else if (cap <= 32) {
-    skinny_rb = cap <= 16 ? 1 : 2;
-  } else if (cap <= 128) {
-    const int64_t pf_wgs = ((cap + 31) / 32) * ((out_cols + 127) / 128);
-    if (pf_wgs < 128 && g.k / 64 >= 48) skinny_rb = 2;
+  } else {
+    skinny_rb = dense_skinny_rows(cap, g.k, g.n, EPI == EPI_STORE && g.splitk_ws != nullptr);
   }
   // the skinny kernel addresses its operands through 2 GiB buffer
   // resources; larger operands go to the tiled kernel where the block size
@@ -948,7 +963,19 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
     return launch_status("w4a16 skinny launch");
   }
   const int dt = std::is_same<T, __bf16>::value ? MXFP4_DT_BF16 : MXFP4_DT_F16;
-  if (pf_supported(g, (int)sizeof(T))) return launch_w4a16_pf(g, dt, EPI, pf_choose(g, EPI), st);
+  if (pf_supported(g, (int)sizeof(T))) {
+    // dense GEMMs too small to fill the chip split K when given a workspace
+    if (EPI == EPI_STORE && !routed && g.splitk_ws != nullptr) {
+      const SplitPlan sp = splitk_plan(g.m, g.k, g.n);
+      if (sp.splits > 1) {
+        GemmArgs gp = g;
+        gp.splitk = sp.splits;
+        const int rc = launch_w4a16_pf(gp, dt, EPI_PARTIAL, sp.cfg, st);
+        return rc ? rc : launch_splitk_reduce(gp, dt, st);
+      }
+    }
+    return launch_w4a16_pf(g, dt, EPI, pf_choose(g, EPI), st);
+  }
   // register-staged kernel: BM must divide block_m (routed); the largest BM
   // that still gives >= 512 workgroups, else the smallest
   const int tile_cols = (EPI == EPI_SILU_MUL) ? 64 : 128;

@@ -85,7 +85,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
   constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
   constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
-  constexpr int C_LD = OUT_COLS * 2 + 16;  // bytes per staged output row
+  constexpr int ES = (EPI == EPI_PARTIAL) ? 4 : 2;  // bytes per output element
+  constexpr int C_LD = OUT_COLS * ES + 16;         // bytes per staged output row
   constexpr int EPI_PASSES = epi_passes(BM, C_LD, S::PIPE);
   constexpr int EPI_ROWS = BM / EPI_PASSES;
   constexpr int SMEM = S::PIPE > EPI_ROWS * C_LD ? S::PIPE : EPI_ROWS * C_LD;
@@ -108,8 +109,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   const int c16 = lane & 15;
   const int grp = lane >> 4;
 
+  // split K: workgroup i computes slice i / (nbm * nbn) of tile i % (nbm * nbn)
+  const int ntile = nbm * nbn;
+  const int split = (EPI == EPI_PARTIAL) ? (int)blockIdx.x / ntile : 0;
   int bm, bn;
-  if (!tile_of(g, BM, nbm, nbn, bm, bn)) return;
+  if (EPI == EPI_PARTIAL) {
+    if (!tile_of(g, BM, nbm, nbn, bm, bn, (int)blockIdx.x % ntile, ntile)) return;
+  } else {
+    if (!tile_of(g, BM, nbm, nbn, bm, bn, blockIdx.x, gridDim.x)) return;
+  }
   const int64_t pos0 = (int64_t)bm * BM;
   const int expert = g.sorted_ids ? block_expert(g, pos0) : 0;
   const int ncol0 = bn * OUT_COLS;
@@ -179,7 +187,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
   }
 
-  const int nk = g.k / 64;
+  // 64-deep stages [k_begin, k_end) of this workgroup's K slice; slices
+  // start on even stages (the scale loads cover stage pairs)
+  int k_begin = 0, k_end = g.k / 64;
+  if (EPI == EPI_PARTIAL) {
+    const int per = ((k_end + g.splitk - 1) / g.splitk + 1) & ~1;
+    k_begin = split * per < k_end ? split * per : k_end;
+    k_end = k_begin + per < k_end ? k_begin + per : k_end;
+  }
   auto issue = [&](int kt) {
     const int st = kt % STAGES;
     if ((kt & 1) == 0) {
@@ -222,8 +237,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
 
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < nk) issue(s);
-  for (int kt = 0; kt < nk; ++kt) {
+    if (k_begin + s < k_end) issue(k_begin + s);
+  for (int kt = k_begin; kt < k_end; ++kt) {
     // Stage kt has landed once at most the later stages' loads are
     // outstanding.  A bare s_barrier (not __syncthreads, whose release fence
     // would drain every outstanding load) then publishes it to all waves and
@@ -231,12 +246,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     // (a wave's loads of one later stage number at most PER_STAGE, plus
     // one scale load on even stages, which waiting for PER_STAGE covers)
     constexpr int PER_STAGE = S::A_PER + S::B_PER;
-    const int later = (nk - 1 - kt) < (STAGES - 2) ? (nk - 1 - kt) : (STAGES - 2);
+    const int later = (k_end - 1 - kt) < (STAGES - 2) ? (k_end - 1 - kt) : (STAGES - 2);
     static_for<0, STAGES - 1>([&](auto c) {
       if (later == decltype(c)::value) wait_vmcnt<decltype(c)::value * PER_STAGE>();
     });
     barrier_only();
-    if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
+    if (kt + STAGES - 1 < k_end) issue(kt + STAGES - 1);
     const uint8_t* As = sA + (kt % STAGES) * S::A_STAGE;
     const uint8_t* Bs = sB + (kt % STAGES) * S::B_STAGE;
     const uint8_t* Ss = sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2;
@@ -276,7 +291,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   // fn*16 + grp*4 .. +3 of its wave's sub-tile; stage the finished rows in
   // LDS and write whole 16-byte chunks
   barrier_only();  // every wave is done reading the stage buffers
-  const float alpha = scalar_alpha(g, expert);
+  // a K slice's partial sums are stored raw; scaling and bias come once,
+  // after the slices are summed
+  const float alpha = (EPI == EPI_PARTIAL) ? 1.0f : scalar_alpha(g, expert);
 #pragma unroll
   for (int pass = 0; pass < EPI_PASSES; ++pass) {
     {
@@ -285,7 +302,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
         if ((wm * FM * 16 + fm * 16) / EPI_ROWS != pass) continue;  // another pass's rows
         const int trow = wm * FM * 16 + fm * 16 + c16;
         float rw = 1.0f;
-        if (g.route_w) {
+        if (EPI == EPI_STORE && g.route_w) {
           const RowInfo r = row_info(g, pos0 + trow);
           rw = r.valid ? g.route_w[r.out_row] : 0.f;
         }
@@ -306,6 +323,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
             }
             *reinterpret_cast<uint2*>(crow + tcol * 2) =
                 uint2{pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
+          }
+        } else if (EPI == EPI_PARTIAL) {
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) {
+            const int tcol = wn * FN * 16 + fn * 16 + grp * 4;
+            *reinterpret_cast<f32x4*>(crow + tcol * 4) = acc[fm][fn];
           }
         } else {
 #pragma unroll
@@ -328,21 +351,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     }
     __syncthreads();
     // whole 16-byte chunks, consecutive lanes along a row
-    constexpr int CHUNKS = OUT_COLS / 8;
+    typedef typename std::conditional<EPI == EPI_PARTIAL, float, T>::type TO;
+    constexpr int VALS = 16 / ES;  // outputs per chunk
+    constexpr int CHUNKS = OUT_COLS / VALS;
+    TO* const cbase = (EPI == EPI_PARTIAL)
+                          ? reinterpret_cast<TO*>(g.splitk_ws + (int64_t)split * g.m * g.n)
+                          : static_cast<TO*>(g.c);
+    const int64_t ldc = (EPI == EPI_PARTIAL) ? (int64_t)g.n : g.ldc;
     for (int idx = tid; idx < EPI_ROWS * CHUNKS; idx += NT) {
       const int prow = idx / CHUNKS, ch = idx % CHUNKS;
       const int trow = pass * EPI_ROWS + prow;
-      const int col = ncol0 + ch * 8;
+      const int col = ncol0 + ch * VALS;
       if (col >= g.n) continue;
       const RowInfo r = row_info(g, pos0 + trow);
       if (!r.valid) continue;
       const uint8_t* src = smem + prow * C_LD + ch * 16;
-      T* dst = static_cast<T*>(g.c) + r.out_row * g.ldc + col;
-      if (col + 8 <= g.n && (g.ldc & 7) == 0) {
+      TO* dst = cbase + r.out_row * ldc + col;
+      if (col + VALS <= g.n && (ldc % VALS) == 0) {
         *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
       } else {
-        const T* s16 = reinterpret_cast<const T*>(src);
-        for (int i = 0; i < 8 && col + i < g.n; ++i) dst[i] = s16[i];
+        const TO* sv = reinterpret_cast<const TO*>(src);
+        for (int i = 0; i < VALS && col + i < g.n; ++i) dst[i] = sv[i];
       }
     }
     if (EPI_PASSES > 1 && pass + 1 < EPI_PASSES) __syncthreads();
@@ -356,7 +385,8 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int nbn = (g.n + out_cols - 1) / out_cols;
   int64_t nbm = (g.m + S::BM - 1) / S::BM;
   if (g.sorted_ids) nbm = (nbm + 7) / 8 * 8;  // every XCD covers 1/8 of the capacity (tile_of)
-  const int64_t nwg = nbm * nbn;
+  int64_t nwg = nbm * nbn;
+  if (EPI == EPI_PARTIAL) nwg *= g.splitk;  // one workgroup per tile and K slice
   if (nwg <= 0 || nwg > 0x7FFFFFFF) {
     set_error("w4a16 prefill: bad grid");
     return MXFP4_ERR_VALUE;
@@ -399,7 +429,7 @@ template <typename T, int EPI>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
     case PF_128x320:
-      if constexpr (EPI == EPI_STORE) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2>(g, st);
+      if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2>(g, st);  // SiLU pairs need even FN
     case PF_128x256: return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2>(g, st);
     case PF_128x128: return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2>(g, st);
@@ -448,11 +478,106 @@ int pf_choose(const GemmArgs& g, int epi) {
 }
 
 int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t st) {
+  if (dtype == MXFP4_DT_BF16) {
+    switch (epi) {
+      case EPI_STORE: return launch_pf_typed<__bf16, EPI_STORE>(g, cfg, st);
+      case EPI_PARTIAL: return launch_pf_typed<__bf16, EPI_PARTIAL>(g, cfg, st);
+      default: return launch_pf_typed<__bf16, EPI_SILU_MUL>(g, cfg, st);
+    }
+  }
+  switch (epi) {
+    case EPI_STORE: return launch_pf_typed<_Float16, EPI_STORE>(g, cfg, st);
+    case EPI_PARTIAL: return launch_pf_typed<_Float16, EPI_PARTIAL>(g, cfg, st);
+    default: return launch_pf_typed<_Float16, EPI_SILU_MUL>(g, cfg, st);
+  }
+}
+
+// ---------------------------------------------------------------- split K
+// Dense GEMMs with few row blocks (mid M, e.g. a 370-token prefill chunk)
+// leave most CUs idle: o_proj M=370 has 192 tiles of 32 x 128 for 256 CUs,
+// each walking 64 stages of K.  Splitting K into S slices gives S times the
+// workgroups (each of K / S), at the price of writing and re-reading
+// S x M x N FP32 partial sums; splitk_reduce adds them in slice order
+// (deterministic), applies the bias and rounds once.
+
+namespace {
+
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, int splits,
+                                                     int64_t m, int n, const T* __restrict__ bias,
+                                                     T* __restrict__ out, int64_t ldc) {
+  const int nq = (n + 3) / 4;
+  const int64_t total = m * nq;
+  const int64_t plane = m * (int64_t)n;
+  const bool vec = (n & 3) == 0;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / nq;
+    const int c = (int)(i % nq) * 4;
+    const float* src = ws + row * n + c;
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    if (vec) {
+      for (int sl = 0; sl < splits; ++sl) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + sl * plane);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] += v[j];
+      }
+    } else {
+      for (int sl = 0; sl < splits; ++sl)
+        for (int j = 0; j < 4 && c + j < n; ++j) o[j] += src[sl * plane + j];
+    }
+    T* dst = out + row * ldc + c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (c + j >= n) break;
+      float v = o[j];
+      if (bias) v += to_f32(bias[c + j]);
+      dst[j] = from_f32<T>(v);
+    }
+  }
+}
+
+}  // namespace
+
+SplitPlan splitk_plan(int64_t m, int64_t k, int64_t n) {
+  // Only where even 32-row tiles would leave CUs idle, and K is long (>= 64
+  // stages) or the tiles very few: with 32 stages, qkv-sized grids (K=2048,
+  // N=5120, M=96-128) run slower split (12.9 -> 15.9 us at M=128).  Tiles
+  // of 32 rows up to M = 256, 64 above; slices double until the grid
+  // reaches 384 workgroups, at most 8 slices of at least 16 stages each (8
+  // while the grid is under 128 workgroups) (steady clocks, bf16, unsplit
+  // -> split: o_proj K=4096 N=2048 M=128 / 200 / 256 / 370: 22.4 / 22.5 /
+  // 22.5 / 22.6 -> 12.6 / 15.6 / 16.8 / 20.3 us; M=130 K=8192 N=640: 43.5
+  // -> 13.4 us; M=64 K=2048 N=1536: 13.1 -> 10.4 us).
+  SplitPlan p{m <= 256 ? PF_32x128 : PF_64x128, 1};
+  const int64_t tiles32 = ((m + 31) / 32) * ((n + 127) / 128);
+  if (tiles32 >= 256 || (k < 4096 && tiles32 >= 64)) return p;
+  const int bm = m <= 256 ? 32 : 64;
+  const int64_t tiles = ((m + bm - 1) / bm) * ((n + 127) / 128);
+  const int64_t nk = k / 64;
+  int s = 1;
+  while (tiles * s < 384 && s < 8 && nk / (2 * s) >= (tiles * s < 128 ? 8 : 16)) s *= 2;
+  p.splits = s;
+  return p;
+}
+
+int64_t splitk_ws_bytes(int64_t m, int64_t k, int64_t n) {
+  if (dense_skinny_rows(m, k, n, true)) return 0;  // the skinny kernel needs none
+  const SplitPlan p = splitk_plan(m, k, n);
+  return p.splits > 1 ? (int64_t)p.splits * m * n * (int64_t)sizeof(float) : 0;
+}
+
+int launch_splitk_reduce(const GemmArgs& g, int dtype, hipStream_t st) {
+  const int64_t total = g.m * ((g.n + 3) / 4);
+  const int64_t blocks = (total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192;
   if (dtype == MXFP4_DT_BF16)
-    return epi == EPI_STORE ? launch_pf_typed<__bf16, EPI_STORE>(g, cfg, st)
-                            : launch_pf_typed<__bf16, EPI_SILU_MUL>(g, cfg, st);
-  return epi == EPI_STORE ? launch_pf_typed<_Float16, EPI_STORE>(g, cfg, st)
-                          : launch_pf_typed<_Float16, EPI_SILU_MUL>(g, cfg, st);
+    splitk_reduce<__bf16><<<(unsigned)blocks, 256, 0, st>>>(
+        g.splitk_ws, g.splitk, g.m, g.n, static_cast<const __bf16*>(g.bias),
+        static_cast<__bf16*>(g.c), g.ldc);
+  else
+    splitk_reduce<_Float16><<<(unsigned)blocks, 256, 0, st>>>(
+        g.splitk_ws, g.splitk, g.m, g.n, static_cast<const _Float16*>(g.bias),
+        static_cast<_Float16*>(g.c), g.ldc);
+  return launch_status("split-K reduce launch");
 }
 
 }  // namespace mx

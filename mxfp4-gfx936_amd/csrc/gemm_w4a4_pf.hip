@@ -93,7 +93,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
   const int grp = lane >> 4;
 
   int bm, bn;
-  if (!tile_of(g, BM, nbm, nbn, bm, bn)) return;
+  if (!tile_of(g, BM, nbm, nbn, bm, bn, blockIdx.x, gridDim.x)) return;
   const int64_t pos0 = (int64_t)bm * BM;
   const int expert = g.sorted_ids ? block_expert(g, pos0) : 0;
   const int ncol0 = bn * BN;

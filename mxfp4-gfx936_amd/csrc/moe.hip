@@ -555,10 +555,27 @@ extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_
   return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int mxfp4_linear_w4a16_workspace_size(int64_t m, int64_t k, int64_t n, int64_t* bytes) {
+  if (bytes == nullptr || m < 0 || k <= 0 || n <= 0) {
+    set_error("linear workspace size: invalid arguments");
+    return MXFP4_ERR_VALUE;
+  }
+  *bytes = (m > 0 && k % 128 == 0) ? splitk_ws_bytes(m, k, n) : 0;
+  return MXFP4_OK;
+}
+
 extern "C" int mxfp4_linear_w4a16(const void* x, int x_dtype, int64_t m, int64_t k,
                                   int64_t x_row_stride, const uint8_t* packed,
                                   const uint8_t* scales, int64_t n, const void* bias, void* out,
                                   void* stream) {
+  return mxfp4_linear_w4a16_ws(x, x_dtype, m, k, x_row_stride, packed, scales, n, bias, out,
+                               nullptr, 0, stream);
+}
+
+extern "C" int mxfp4_linear_w4a16_ws(const void* x, int x_dtype, int64_t m, int64_t k,
+                                     int64_t x_row_stride, const uint8_t* packed,
+                                     const uint8_t* scales, int64_t n, const void* bias, void* out,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
   if (x_dtype != MXFP4_DT_BF16 && x_dtype != MXFP4_DT_F16) {
     set_error("x must be fp16 or bf16, got dtype %d", x_dtype);
     return MXFP4_ERR_TYPE;
@@ -593,6 +610,14 @@ extern "C" int mxfp4_linear_w4a16(const void* x, int x_dtype, int64_t m, int64_t
   g.k = (int32_t)k;
   g.top_k = 1;
   g.block_m = 16;
+  if (workspace != nullptr) {
+    const int64_t need = splitk_ws_bytes(m, k, n);
+    if (need > 0 && (workspace_bytes < need || !aligned16(workspace))) {
+      set_error("linear: workspace must be 16-byte aligned and hold %lld bytes", (long long)need);
+      return MXFP4_ERR_VALUE;
+    }
+    if (need > 0) g.splitk_ws = static_cast<float*>(workspace);
+  }
   return launch_w4a16(g, x_dtype, EPI_STORE, static_cast<hipStream_t>(stream));
 }
 

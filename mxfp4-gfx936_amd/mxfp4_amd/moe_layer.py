@@ -82,7 +82,7 @@ def moe_layer(
     _lib.check(lib.mxfp4_moe_layer_workspace_size(m, top_k, num_experts, hidden, inter,
                                                   ctypes.byref(nbytes)))
     ws = torch.empty(nbytes.value, dtype=torch.uint8, device=device)
-    with torch.cuda.device(device):
+    with _lib.on_device(device):
         _lib.check(lib.mxfp4_moe_layer(
             _lib.ptr(xc), _lib.dtype_code(x.dtype), m, hidden, _lib.ptr(_lib.aligned(w13)),
             _lib.ptr(w13_scale.contiguous()), _lib.ptr(_lib.aligned(w2)),

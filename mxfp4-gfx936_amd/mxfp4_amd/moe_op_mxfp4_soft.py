@@ -15,6 +15,7 @@ path with importlib, as the reference tests load their module (test:10-19).
 
 from __future__ import annotations
 
+import ctypes
 import os
 import sys
 
@@ -91,11 +92,28 @@ def dequant_mxfp4(
     if rows and logical_k:
         p = _lib.aligned(packed.reshape(rows, logical_k // 2))
         s = block_scales.reshape(rows, logical_k // 32).contiguous()
-        with torch.cuda.device(device):
+        with _lib.on_device(device):
             _lib.check(lib.mxfp4_dequant(
                 _lib.ptr(p), p.stride(0), _lib.ptr(s), s.stride(0), rows, logical_k,
                 _lib.ptr(out), _lib.dtype_code(kernel_dtype), _lib.stream_of(device)))
     return out if kernel_dtype == dtype else out.to(dtype)
+
+
+_LINEAR_WS: dict = {}
+
+
+def _linear_workspace_bytes(lib, m: int, k: int, n: int) -> int:
+    """Split-K workspace bytes of the dense linear (a pure function of the
+    sizes, cached)."""
+    key = (m, k, n)
+    v = _LINEAR_WS.get(key)
+    if v is None:
+        out = ctypes.c_int64(0)
+        _lib.check(lib.mxfp4_linear_w4a16_workspace_size(m, k, n, ctypes.byref(out)))
+        if len(_LINEAR_WS) >= 4096:
+            _LINEAR_WS.clear()
+        v = _LINEAR_WS[key] = out.value
+    return v
 
 
 def linear_mxfp4_soft(
@@ -138,11 +156,14 @@ def linear_mxfp4_soft(
     b = bias.contiguous() if fuse_bias else None
     output = torch.empty((x_2d.shape[0], n), dtype=x.dtype, device=device)
     if x_2d.shape[0] and n:
-        with torch.cuda.device(device):
-            _lib.check(lib.mxfp4_linear_w4a16(
+        # GEMMs too small to fill the GPU split K through a workspace
+        ws_bytes = _linear_workspace_bytes(lib, x_2d.shape[0], logical_k, n)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+        with _lib.on_device(device):
+            _lib.check(lib.mxfp4_linear_w4a16_ws(
                 _lib.ptr(x_2d), _lib.dtype_code(x.dtype), x_2d.shape[0], logical_k,
                 x_2d.stride(0), _lib.ptr(w), _lib.ptr(s), n, _lib.ptr(b), _lib.ptr(output),
-                _lib.stream_of(device)))
+                _lib.ptr(ws), ws_bytes, _lib.stream_of(device)))
     if bias is not None and not fuse_bias:
         output = output + bias
     return output.reshape(*input_shape[:-1], n)
@@ -168,7 +189,7 @@ def make_routing_device(topk_ids: torch.Tensor, num_experts: int, block_m: int):
     expert_ids = torch.empty(mb.value, dtype=torch.int32, device=device)
     npp = torch.empty(1, dtype=torch.int32, device=device)
     ws = torch.empty(max(wsb.value // 4, 1), dtype=torch.int32, device=device)
-    with torch.cuda.device(device):
+    with _lib.on_device(device):
         _lib.check(lib.mxfp4_moe_align(
             _lib.ptr(ids), _lib.dtype_code(ids.dtype), n, num_experts, block_m,
             _lib.ptr(sorted_ids), _lib.ptr(expert_ids), _lib.ptr(npp), _lib.ptr(ws),
@@ -185,7 +206,7 @@ def _moe_gemm_launch(A, A_mx_scale, B, B_mx_scale, C2d, A_scale, B_scale, topk_w
     num_experts, n, k = B.shape[0], B.shape[1], B.shape[2] * 2
     a_code = _lib.dtype_code(A.dtype)
     a_row_stride = A.stride(0)
-    with torch.cuda.device(device):
+    with _lib.on_device(device):
         _lib.check(lib.mxfp4_moe_gemm(
             _lib.ptr(A), a_code, A.shape[0], a_row_stride, _lib.ptr(A_mx_scale), _lib.ptr(B),
             _lib.ptr(B_mx_scale), num_experts, n, k, _lib.ptr(C2d), _lib.dtype_code(C2d.dtype),

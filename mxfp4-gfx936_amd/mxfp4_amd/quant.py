@@ -44,7 +44,7 @@ def dynamic_mxfp4_quant(x: torch.Tensor, mode: str = "ties_away"):
         x2 = x.reshape(rows, k)
         if x2.stride(-1) != 1:
             x2 = x2.contiguous()
-        with torch.cuda.device(device):
+        with _lib.on_device(device):
             _lib.check(lib.mxfp4_quant(
                 _lib.ptr(x2), _lib.dtype_code(x.dtype), rows, k, x2.stride(0), _MODES[mode],
                 _lib.ptr(packed), _lib.ptr(scales), _lib.stream_of(device)))
@@ -76,7 +76,7 @@ def linear_mxfp4_w4a4(a_packed: torch.Tensor, a_scales: torch.Tensor, w_packed: 
     if m and n:
         a = _lib.aligned(a_packed)
         w = _lib.aligned(w_packed)
-        with torch.cuda.device(device):
+        with _lib.on_device(device):
             _lib.check(lib.mxfp4_linear_w4a4(
                 _lib.ptr(a), _lib.ptr(a_scales.contiguous()), m, k, _lib.ptr(w),
                 _lib.ptr(w_scales.contiguous()), n, _lib.ptr(out), _lib.dtype_code(out_dtype),

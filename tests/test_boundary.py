@@ -37,6 +37,31 @@ def test_library_exports_every_declared_symbol():
     assert lib.mxfp4_abi_version() == _lib.ABI_VERSION
 
 
+def _split_ws(m, k, n):
+    out = ctypes.c_int64(-1)
+    assert _lib.load().mxfp4_linear_w4a16_workspace_size(m, k, n, ctypes.byref(out)) == _lib.OK
+    return out.value
+
+
+def test_linear_split_k_workspace_plan():
+    # the dense linear splits K (FP32 slices in a caller workspace) only for
+    # grids that would leave CUs idle; decode sizes and full grids need none
+    assert _split_ws(1, 4096, 2048) == 0          # skinny decode kernel
+    assert _split_ws(48, 4096, 2048) == 0         # 32-row skinny blocks
+    assert _split_ws(4096, 2048, 5120) == 0       # the headline fills the GPU
+    assert _split_ws(370, 2048, 5120) == 0        # 480 tiles of 32 rows
+    assert _split_ws(128, 2048, 5120) == 0        # short K: slices do not pay
+    assert _split_ws(370, 4096, 2048) == 4 * 370 * 2048 * 4
+    assert _split_ws(128, 4096, 2048) == 4 * 128 * 2048 * 4
+    assert _split_ws(200, 4096, 2048) == 4 * 200 * 2048 * 4
+    assert _split_ws(130, 8192, 640) == 8 * 130 * 640 * 4
+    assert _split_ws(64, 2048, 1536) == 4 * 64 * 1536 * 4
+    assert _split_ws(64, 8192, 1024) > 0          # long K: split beats skinny
+    out = ctypes.c_int64(0)
+    assert _lib.load().mxfp4_linear_w4a16_workspace_size(-1, 128, 8, ctypes.byref(out)) \
+        == _lib.ERR_VALUE
+
+
 def test_c_abi_argument_errors_without_launch():
     lib = _lib.load()
     null = ctypes.c_void_p()

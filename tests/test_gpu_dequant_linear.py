@@ -4,6 +4,7 @@
 
 from __future__ import annotations
 
+import ctypes
 import os
 
 import numpy as np
@@ -171,6 +172,28 @@ def test_linear_mid_m_long_k(m):
     ref = _safe_reference(cuda(x), packed, scales)
     oracle = O.linear_fp64(x.float().numpy(), packed, scales)
     assert_parity(y, oracle, ref=ref, what=f"mid m={m}")
+
+
+@pytest.mark.parametrize("m,k,n,dt", [(370, 4096, 2048, torch.bfloat16),
+                                      (200, 4096, 1002, torch.float16),
+                                      (64, 2048, 1536, torch.bfloat16),
+                                      (130, 8192, 640, torch.bfloat16)])
+def test_linear_split_k(m, k, n, dt):
+    # too few tiles to fill the GPU: K goes in slices whose FP32 partial sums
+    # are added in slice order, then the bias, then one rounding
+    ws = ctypes.c_int64(0)
+    _lib.check(_lib.load().mxfp4_linear_w4a16_workspace_size(m, k, n, ctypes.byref(ws)))
+    assert ws.value >= 2 * m * n * 4, "this shape is expected to split K"
+    rng = np.random.default_rng(500 + m)
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    x = rand_act(500 + m, (m, k), dt)
+    bias = rand_act(501 + m, (n,), dt)
+    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales), cuda(bias))
+    assert y.dtype == dt and y.shape == (m, n)
+    oracle = O.linear_fp64(x.float().numpy(), packed, scales, bias.float().numpy())
+    assert_parity(y, oracle, what=f"split-K m={m} k={k} n={n}")
+    y2 = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales), cuda(bias))
+    assert torch.equal(y, y2)  # deterministic
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
