@@ -96,6 +96,86 @@ __global__ __launch_bounds__(256) void quant_kernel(const T* __restrict__ x, int
   }
 }
 
+// RNE quantizer for 16-bit inputs on gfx950's FP4 encoder.
+// v_cvt_scalef32_pk_fp4_{bf16,f16}(pair, 2^E) equals code_rne(x * 2^-E) for
+// every non-NaN bf16 / f16 value and every E in [-127, 127] (checked on the
+// device, exhaustively), and writes its two nibbles into a chosen byte of
+// the destination, so one instruction handles two elements and packs them.
+// Four consecutive lanes share a 32-block (16 bytes of input each: 1 KB per
+// wave load, 256 contiguous output bytes per wave store); the block amax is
+// an integer max of the magnitude bits (their order is the float order
+// below NaN), reduced over the four lanes.  A block holding a NaN takes the
+// scalar path above, so NaN handling is unchanged (ignored by the amax, code
+// = its sign).  Needs 16-byte aligned rows.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_rne16(const T* __restrict__ x, int64_t rows, int64_t k,
+                                                   int64_t ldx, uint8_t* __restrict__ packed,
+                                                   uint8_t* __restrict__ scales) {
+  static_assert(sizeof(T) == 2, "16-bit inputs");
+  constexpr uint32_t kInf = std::is_same<T, __bf16>::value ? 0x7F80u : 0x7C00u;
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  const int64_t bpr = k >> 5;
+  const int64_t total = rows * bpr;
+  const int q = threadIdx.x & 3;
+  for (int64_t u = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 2; u < total;
+       u += (int64_t)gridDim.x * 64) {
+    const int64_t r = u / bpr;
+    const int64_t b = u - r * bpr;
+    const T* src = x + r * ldx + b * 32 + q * 8;
+    const i32x4 w = *reinterpret_cast<const i32x4*>(src);
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = (uint32_t)w[j] & 0x7FFF7FFFu;
+      const uint32_t lo = a & 0xFFFFu, hi = a >> 16;
+      m = m > lo ? m : lo;
+      m = m > hi ? m : hi;
+    }
+    uint32_t o = (uint32_t)__shfl_xor((int)m, 1);
+    m = m > o ? m : o;
+    o = (uint32_t)__shfl_xor((int)m, 2);
+    m = m > o ? m : o;
+    uint32_t word = 0;
+    int e;
+    if (m <= kInf) {
+      const float amax = std::is_same<T, __bf16>::value
+                             ? __uint_as_float(m << 16)
+                             : (float)__builtin_bit_cast(_Float16, (uint16_t)m);
+      if (amax == 0.f) e = -127;
+      else if (isinf(amax)) e = 127;
+      else e = clamp_e(floor_log2(amax) - 2);
+      const float sc = pow2_f32(e);
+      static_for<0, 4>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        // (int) first: this clang bit-casts an element of a vector lvalue as
+        // element 0, whatever the index
+        const T2 v = __builtin_bit_cast(T2, (int)w[j]);
+        if constexpr (std::is_same<T, __bf16>::value)
+          word = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(word, v, sc, j);
+        else
+          word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f16(word, v, sc, j);
+      });
+    } else {  // a NaN in the block: the scalar rule
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (float)src[j];
+      float amax = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+      amax = fmaxf(amax, __shfl_xor(amax, 1));
+      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      if (amax == 0.f) e = -127;
+      else if (isinf(amax)) e = 127;
+      else e = clamp_e(floor_log2(amax) - 2);
+      const float inv = pow2_f32(-e);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) word |= (code_rne(v[j] * inv) & 15u) << (j * 4);
+    }
+    *reinterpret_cast<uint32_t*>(packed + r * (k >> 1) + b * 16 + q * 4) = word;
+    if (q == 0) scales[r * bpr + b] = (uint8_t)((e + 127) & 0xFF);
+  }
+}
+
 template <typename T>
 void launch_quant_typed(const void* x, int64_t rows, int64_t k, int64_t ldx, int mode,
                         uint8_t* packed, uint8_t* scales, int grid, hipStream_t st) {
@@ -134,6 +214,18 @@ extern "C" int mxfp4_quant(const void* x, int x_dtype, int64_t rows, int64_t k,
   if (total == 0) return MXFP4_OK;
   const int grid = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // 16-bit inputs with 16-byte aligned rows: the RNE rule on the FP4 encoder
+  const bool rows16 = ((reinterpret_cast<uintptr_t>(x) | (uintptr_t)(x_row_stride * 2)) & 15) == 0;
+  if (mode == MXFP4_QUANT_RNE && x_dtype != MXFP4_DT_F32 && rows16) {
+    const int g16 = (int)((total + 63) / 64 < 16384 ? (total + 63) / 64 : 16384);
+    if (x_dtype == MXFP4_DT_BF16)
+      quant_rne16<__bf16><<<g16, 256, 0, st>>>(static_cast<const __bf16*>(x), rows, k, x_row_stride,
+                                               packed, scales);
+    else
+      quant_rne16<_Float16><<<g16, 256, 0, st>>>(static_cast<const _Float16*>(x), rows, k,
+                                                 x_row_stride, packed, scales);
+    return launch_status("quant launch");
+  }
   switch (x_dtype) {
     case MXFP4_DT_BF16:
       launch_quant_typed<__bf16>(x, rows, k, x_row_stride, mode, packed, scales, grid, st);

@@ -33,6 +33,41 @@ def test_quant_matches_oracle(mode, dtype):
     assert np.array_equal(p.cpu().numpy(), rp) and np.array_equal(s.cpu().numpy(), rs)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quant_rne_encoder_path_matches_scalar_path(dtype):
+    # 16-bit inputs with aligned rows take the FP4-encoder kernel; a view
+    # one element off the alignment takes the scalar kernel.  Both must give
+    # the same bytes, also for NaN, inf, subnormal and all-zero blocks.
+    g = torch.Generator().manual_seed(7)
+    rows, k = 96, 1024
+    x = torch.randn((rows, k), generator=g) * torch.exp2(
+        torch.randint(-30, 30, (rows, k // 32), generator=g).float()).repeat_interleave(32, 1)
+    x = x.to(dtype)
+    info = torch.finfo(dtype)
+    x[0, 5] = float("nan")
+    x[1, :32] = float("nan")
+    x[2, 7] = float("inf")
+    x[3, 9] = -float("inf")
+    x[4, :32] = 0.0
+    x[5, :32] = info.tiny * torch.linspace(-1, 1, 32).to(dtype)  # near the subnormal range
+    x[6, :32] = info.max
+    x[7, 0] = -0.0
+    x[8, 40] = float("nan")
+    x[8, 41] = info.max
+    big = torch.zeros((rows, k + 8), dtype=dtype)
+    big[:, 1:1 + k] = x
+    xa = cuda(x)
+    xm = cuda(big)[:, 1:1 + k]  # base pointer 2 bytes off a 16-byte boundary
+    assert xa.data_ptr() % 16 == 0 and xm.data_ptr() % 16 == 2
+    pa, sa = mx.dynamic_mxfp4_quant(xa, mode="rne")
+    pm, sm = mx.dynamic_mxfp4_quant(xm, mode="rne")
+    assert torch.equal(pa, pm) and torch.equal(sa, sm)
+    finite = torch.isfinite(x).all(dim=1)
+    rp, rs = c_oracle.quant(x[finite].float().numpy(), "rne")
+    assert np.array_equal(pa[cuda(finite)].cpu().numpy(), rp)
+    assert np.array_equal(sa[cuda(finite)].cpu().numpy(), rs)
+
+
 def test_quant_golden_fixture():
     g = np.load(os.path.join(GOLDEN, "small_cases.npz"))
     x = cuda(g["quant_x"])
