@@ -17,11 +17,14 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
                                                       int64_t sstride, int64_t rows, int64_t k,
                                                       void* __restrict__ out) {
   const int64_t units_per_row = k >> 3;  // 8 values per unit
-  const int64_t total = rows * units_per_row;
-  const int64_t step = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += step) {
-    const int64_t r = u / units_per_row;
-    const int64_t c = u - r * units_per_row;
+  // a workgroup takes 256 consecutive units of one row, so the row index is
+  // one scalar division per workgroup step, not a 64-bit division per lane
+  const int64_t chunks = (units_per_row + 255) >> 8;  // per row
+  const int64_t total = rows * chunks;
+  for (int64_t gch = blockIdx.x; gch < total; gch += gridDim.x) {
+    const int64_t r = gch / chunks;
+    const int64_t c = (gch - r * chunks) * 256 + threadIdx.x;
+    if (c >= units_per_row) continue;
     const uint32_t p = *reinterpret_cast<const uint32_t*>(packed + r * pstride + c * 4);
     const uint32_t s = scales[r * sstride + (c >> 2)];
     const int64_t o = r * k + c * 8;
@@ -79,7 +82,7 @@ extern "C" int mxfp4_dequant(const uint8_t* packed, int64_t packed_row_stride,
   }
   const int64_t total = rows * (k / 8);
   if (total == 0) return MXFP4_OK;
-  const int64_t want = (total + 255) / 256;
+  const int64_t want = rows * ((k / 8 + 255) / 256);  // workgroup steps
   const int grid = (int)(want < 16384 ? want : 16384);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (out_dtype) {
