@@ -21,6 +21,8 @@
 // * Epilogue.  Scales / route weight / bias / SiLU*mul are applied in
 //   registers, the tile is staged in LDS (reusing the stage buffers) and
 //   written back as full 16-byte chunks, whole output rows per instruction.
+//   EPI_PARTIAL (split K) instead stores the raw FP32 sums of one K slice;
+//   splitk_reduce (below) adds the slices.
 // * Order.  Workgroups are dealt round-robin over the 8 XCDs; tile_of
 //   (gemm.h) gives each XCD a contiguous range of rows.
 //
