@@ -12,6 +12,9 @@ current stream; no host synchronisation, no fallback path):
   metadata (integration/vllm/vllm_mxfp4_gfx936.py:119-146, 233-265);
 * ``dynamic_mxfp4_quant`` / ``linear_mxfp4_w4a4`` -- activation quantizer
   and dense W4A4 on the block-scaled FP4 MFMA.
+
+``mxfp4_amd.vllm_adapter.install()`` points vLLM's compressed-tensors MXFP4
+schemes at these operators (integration/vllm/vllm_mxfp4_gfx936.py).
 """
 
 from .moe_op_mxfp4_soft import (  # noqa: F401

@@ -1,0 +1,116 @@
+"""vLLM hooks: the compressed-tensors MXFP4 schemes on the gfx950 backend.
+
+Mirrors the reference adapter ``integration/vllm/vllm_mxfp4_gfx936.py``
+(vllm:1-275): the same two schemes are patched with functions of the same
+names and meaning,
+
+* ``CompressedTensorsW4A16Mxfp4`` (dense W4A16 layers):
+  ``process_weights_after_loading`` (vllm:68-70) and ``apply_weights``
+  (vllm:105-116) -> ``linear_mxfp4_soft``;
+* ``CompressedTensorsW4A4Mxfp4MoEMethod`` (the MoE layers):
+  ``process_weights_after_loading`` (vllm:215-230) and ``apply``
+  (vllm:233-265) -> ``moe_layer`` (device routing, gate_up with SiLU*mul,
+  down with the route weight, top-k sum; no host synchronisation).
+
+Call ``install()`` before constructing ``vllm.LLM``.  ``install(dense_cls,
+moe_cls)`` patches the given classes instead of importing vLLM's (how the
+tests exercise it without vLLM).  ``MXFP4_IMPLEMENTATION`` keeps the
+reference's validation (vllm:28-36): ``safe`` and ``triton`` both run the
+HIP kernels; the reference's ``reference`` / ``bf16`` debug path (a torch
+bf16 GEMM on dequantized weights) has no counterpart here and is refused, as
+is any other value.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+from torch.nn.parameter import Parameter
+
+from .moe_layer import moe_layer
+from .moe_op_mxfp4_soft import linear_mxfp4_soft
+
+MIN_VLLM = (0, 15, 0)  # vllm:24-27
+
+
+def _implementation() -> str:
+    impl = os.getenv("MXFP4_IMPLEMENTATION", "safe")
+    if impl in ("reference", "bf16"):
+        raise ValueError(
+            "MXFP4_IMPLEMENTATION=reference (the bf16 debug path) is not provided by the "
+            "gfx950 backend; use safe or triton")
+    if impl not in ("safe", "triton"):
+        raise ValueError(f"unknown MXFP4 implementation: {impl}")
+    return impl
+
+
+def _dense_process_weights_after_loading(self, layer):
+    """vllm:68-70: plain frozen parameters for the packed weight and scales."""
+    del self
+    layer.weight_packed = Parameter(layer.weight_packed.data, requires_grad=False)
+    layer.weight_scale = Parameter(layer.weight_scale.data, requires_grad=False)
+
+
+def _dense_apply_weights(self, layer, x, bias=None, input_quant_args=None,
+                         silu_quant_args=None):
+    """vllm:105-116: x @ dequant(weight).T (+ bias) on the W4A16 kernels."""
+    del self, input_quant_args, silu_quant_args
+    return linear_mxfp4_soft(x, layer.weight_packed, layer.weight_scale, bias)
+
+
+def _moe_process_weights_after_loading(self, layer):
+    """vllm:215-230: the packed expert weights become ``w13_weight`` /
+    ``w2_weight`` (frozen); the ``*_packed`` attributes are removed."""
+    del self
+    layer.w13_weight = Parameter(layer.w13_weight_packed.data, requires_grad=False)
+    layer.w13_weight_scale = Parameter(layer.w13_weight_scale.data, requires_grad=False)
+    layer.w2_weight = Parameter(layer.w2_weight_packed.data, requires_grad=False)
+    layer.w2_weight_scale = Parameter(layer.w2_weight_scale.data, requires_grad=False)
+    delattr(layer, "w13_weight_packed")
+    delattr(layer, "w2_weight_packed")
+
+
+def _moe_apply(self, layer, x, topk_weights, topk_ids, use_nn_moe=False):
+    """vllm:233-265: the routed MoE layer for [tokens, hidden] activations."""
+    del self, use_nn_moe
+    if layer.activation != "silu":
+        raise NotImplementedError(
+            f"the gfx936 MXFP4 adapter supports silu, got {layer.activation}")
+    return moe_layer(x, layer.w13_weight, layer.w13_weight_scale, layer.w2_weight,
+                     layer.w2_weight_scale, topk_weights, topk_ids, activation=layer.activation)
+
+
+def _vllm_classes():
+    try:
+        import vllm
+        from vllm.model_executor.layers.quantization.compressed_tensors.compressed_tensors_moe import (  # noqa: E501
+            CompressedTensorsW4A4Mxfp4MoEMethod,
+        )
+        from vllm.model_executor.layers.quantization.compressed_tensors.schemes.compressed_tensors_w4a16_mxfp4 import (  # noqa: E501
+            CompressedTensorsW4A16Mxfp4,
+        )
+    except ImportError as e:
+        raise ImportError(f"the gfx950 MXFP4 adapter needs vLLM >= 0.15: {e}") from e
+    version = tuple(int(p) for p in vllm.__version__.split("+")[0].split(".")[:3] if p.isdigit())
+    if version < MIN_VLLM:
+        raise RuntimeError(f"the gfx950 MXFP4 adapter requires vLLM >= 0.15, got {vllm.__version__}")
+    return CompressedTensorsW4A16Mxfp4, CompressedTensorsW4A4Mxfp4MoEMethod
+
+
+def install(dense_cls=None, moe_cls=None) -> str:
+    """Patch the dense and MoE scheme classes (vllm:268-275); returns the
+    implementation name.  With no arguments the classes come from vLLM."""
+    impl = _implementation()
+    if dense_cls is None or moe_cls is None:
+        d, m = _vllm_classes()
+        dense_cls = d if dense_cls is None else dense_cls
+        moe_cls = m if moe_cls is None else moe_cls
+    # the operators read this switch too (soft:45-49)
+    os.environ["MXFP4_GFX936_BACKEND"] = impl
+    dense_cls.process_weights_after_loading = _dense_process_weights_after_loading
+    dense_cls.apply_weights = _dense_apply_weights
+    moe_cls.process_weights_after_loading = _moe_process_weights_after_loading
+    moe_cls.apply = _moe_apply
+    print(f"MXFP4_GFX950_ADAPTER_ACTIVE torch={torch.__version__} implementation={impl}")
+    return impl

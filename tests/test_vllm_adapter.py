@@ -1,0 +1,98 @@
+"""The vLLM adapter (mxfp4_amd.vllm_adapter) on the CPU with fake scheme
+classes and layers: what it patches (vllm:268-275), the weight renames of
+process_weights_after_loading (vllm:68-70, 215-230), the implementation switch
+(vllm:28-36), and that apply / apply_weights hand the layer's tensors to
+linear_mxfp4_soft / moe_layer (recorded here; the operators themselves are
+covered by the GPU tests).  vLLM is not installed in this image."""
+
+from __future__ import annotations
+
+import types
+
+import pytest
+import torch
+
+from mxfp4_amd import vllm_adapter as va
+
+
+@pytest.fixture(autouse=True)
+def _restore_backend_switch(monkeypatch):
+    # install() sets MXFP4_GFX936_BACKEND for the operators; monkeypatch
+    # restores it after each test
+    monkeypatch.setenv("MXFP4_GFX936_BACKEND", "safe")
+
+
+class _Dense:
+    pass
+
+
+class _MoE:
+    pass
+
+
+def test_install_patches_both_schemes(monkeypatch, capsys):
+    monkeypatch.delenv("MXFP4_IMPLEMENTATION", raising=False)
+    assert va.install(_Dense, _MoE) == "safe"
+    assert _Dense.process_weights_after_loading is va._dense_process_weights_after_loading
+    assert _Dense.apply_weights is va._dense_apply_weights
+    assert _MoE.process_weights_after_loading is va._moe_process_weights_after_loading
+    assert _MoE.apply is va._moe_apply
+    assert "MXFP4_GFX950_ADAPTER_ACTIVE" in capsys.readouterr().out
+
+
+@pytest.mark.parametrize("impl,ok", [("safe", True), ("triton", True), ("reference", False),
+                                     ("bf16", False), ("cuda", False)])
+def test_implementation_switch(monkeypatch, impl, ok):
+    monkeypatch.setenv("MXFP4_IMPLEMENTATION", impl)
+    if ok:
+        assert va.install(_Dense, _MoE) == impl
+    else:
+        with pytest.raises(ValueError):
+            va.install(_Dense, _MoE)
+
+
+def test_install_without_vllm_says_so(monkeypatch):
+    monkeypatch.delenv("MXFP4_IMPLEMENTATION", raising=False)
+    with pytest.raises(ImportError, match="vLLM"):
+        va.install()
+
+
+def test_dense_weights_become_frozen_parameters():
+    layer = types.SimpleNamespace(weight_packed=torch.zeros(4, 16, dtype=torch.uint8),
+                                  weight_scale=torch.full((4, 1), 127, dtype=torch.uint8))
+    va._dense_process_weights_after_loading(object(), layer)
+    for t in (layer.weight_packed, layer.weight_scale):
+        assert isinstance(t, torch.nn.Parameter) and not t.requires_grad
+    assert layer.weight_packed.dtype == torch.uint8
+
+
+def test_moe_weights_renamed_like_the_reference():
+    layer = types.SimpleNamespace(
+        w13_weight_packed=torch.zeros(2, 64, 16, dtype=torch.uint8),
+        w13_weight_scale=torch.zeros(2, 64, 1, dtype=torch.uint8),
+        w2_weight_packed=torch.zeros(2, 32, 16, dtype=torch.uint8),
+        w2_weight_scale=torch.zeros(2, 32, 1, dtype=torch.uint8))
+    va._moe_process_weights_after_loading(object(), layer)
+    assert not hasattr(layer, "w13_weight_packed") and not hasattr(layer, "w2_weight_packed")
+    for name in ("w13_weight", "w13_weight_scale", "w2_weight", "w2_weight_scale"):
+        t = getattr(layer, name)
+        assert isinstance(t, torch.nn.Parameter) and not t.requires_grad
+    assert layer.w13_weight.shape == (2, 64, 16) and layer.w2_weight.shape == (2, 32, 16)
+
+
+def test_apply_paths_call_the_operators(monkeypatch):
+    calls = []
+    monkeypatch.setattr(va, "linear_mxfp4_soft", lambda *a: calls.append(("linear", a)) or "y")
+    monkeypatch.setattr(va, "moe_layer",
+                        lambda *a, **k: calls.append(("moe", a, k)) or "z")
+    dense = types.SimpleNamespace(weight_packed="W", weight_scale="S")
+    assert va._dense_apply_weights(object(), dense, "x", "b", input_quant_args=1,
+                                   silu_quant_args=2) == "y"
+    assert calls[-1] == ("linear", ("x", "W", "S", "b"))
+    moe = types.SimpleNamespace(activation="silu", w13_weight="A", w13_weight_scale="As",
+                                w2_weight="B", w2_weight_scale="Bs")
+    assert va._moe_apply(object(), moe, "x", "tw", "ti", use_nn_moe=True) == "z"
+    assert calls[-1] == ("moe", ("x", "A", "As", "B", "Bs", "tw", "ti"), {"activation": "silu"})
+    moe.activation = "gelu"
+    with pytest.raises(NotImplementedError, match="silu"):
+        va._moe_apply(object(), moe, "x", "tw", "ti")
