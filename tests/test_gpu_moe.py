@@ -256,6 +256,27 @@ def test_moe_layer_vs_oracle(m, layer_weights):
     assert_layer_parity(y[t(rows).cuda()], oracle, safe, what=f"moe layer m={m}")
 
 
+def test_vllm_adapter_moe_and_dense_on_device(layer_weights):
+    # the vLLM hooks on real layers: weights renamed as vllm:215-230, then
+    # apply / apply_weights equal the operators they wrap, bit for bit
+    import types
+    from mxfp4_amd import vllm_adapter as va
+    w13, s13, w2, s2 = layer_weights
+    layer = types.SimpleNamespace(activation="silu", w13_weight_packed=cuda(w13),
+                                  w13_weight_scale=cuda(s13), w2_weight_packed=cuda(w2),
+                                  w2_weight_scale=cuda(s2))
+    va._moe_process_weights_after_loading(None, layer)
+    x = cuda(rand_act(71, (8, 2048)))
+    w, ids = _route(8, 128, 8, 72)
+    y = va._moe_apply(None, layer, x, cuda(w), cuda(ids))
+    ref = mx.moe_layer(x, cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
+    assert torch.equal(y, ref)
+    dense = types.SimpleNamespace(weight_packed=cuda(w13[0]), weight_scale=cuda(s13[0]))
+    va._dense_process_weights_after_loading(None, dense)
+    yd = va._dense_apply_weights(None, dense, x)
+    assert torch.equal(yd, mx.linear_mxfp4_soft(x, cuda(w13[0]), cuda(s13[0])))
+
+
 def test_moe_layer_hidden_not_multiple_of_128():
     # hidden 1056 (K % 128 == 32 for gate_up): routed blocks of 64 go to the
     # register-staged tiled kernel; inter 320 keeps the down GEMM on it too
