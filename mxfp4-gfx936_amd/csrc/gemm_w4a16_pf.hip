@@ -475,7 +475,11 @@ int pf_choose(const GemmArgs& g, int epi) {
     if (f256 >= 0.8) return PF_128x256;
     if (tiles(128, 128) >= 512) return PF_128x128;
   }
-  if (allowed(64) && tiles(64, 128) >= 512) return PF_64x128;
+  // 64-row waves halve the decode work per MFMA of 32-row ones; they win
+  // from ~200 tiles (qkv K=2048 N=5120, steady clocks: M=370 18.1 -> 16.8
+  // us, M=512 23.8 -> 20.7 us; M=256, 160 tiles, stays with 32 rows: 15.6
+  // vs 17.8 us)
+  if (allowed(64) && tiles(64, 128) >= 200) return PF_64x128;
   return PF_32x128;
 }
 
