@@ -81,9 +81,45 @@ constexpr int epi_passes(int bm, int row_bytes, int pipe_bytes) {
   return p;
 }
 
+// One 64-deep stage of a wave's FM x FN block of 16 x 16 outputs: all LDS
+// reads of the stage first (the reads of ks = 1 overlap the MFMAs of ks = 0),
+// then per ks: decode every weight fragment, then the FM x FN MFMAs back to
+// back.  Logical chunk ks*4 + grp of an A row sits at physical chunk (grp ^
+// sw) ^ (ks*4): flipping bit 6 of the byte offset selects the ks = 1 half.
+// Ss points at the stage's two scale bytes of the wave's first weight row.
+template <typename T, int FM, int FN>
+__device__ __forceinline__ void stage_math(const uint8_t* As, const uint8_t* Bs, const uint8_t* Ss,
+                                           int a_rd0, int b_rd, int b_sw, int s_rd,
+                                           f32x4 (&acc)[FM][FN]) {
+  typedef typename V8Of<T>::type V8;
+  V8 af[2][FM];
+  uint32_t raw[2][FN];
+  uint32_t sb[2][FN];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+      af[ks][fm] = *reinterpret_cast<const V8*>(As + ((a_rd0 + fm * 16 * 128) ^ (ks * 64)));
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      raw[ks][fn] = *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 16 * 32 + ((ks ^ b_sw) * 16));
+      sb[ks][fn] = Ss[s_rd + fn * 16 * 4 + ks];
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    V8 bf[FN];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) bf[fn] = Decode<T>::run(raw[ks][fn], e8m0_scale(sb[ks][fn]));
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) acc[fm][fn] = mfma16(bf[fn], af[ks][fm], acc[fm][fn]);
+  }
+}
+
 template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB>
 __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int nbm, int nbn) {
-  typedef typename V8Of<T>::type V8;
   typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
   constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
   constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
@@ -254,39 +290,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     });
     barrier_only();
     if (kt + STAGES - 1 < k_end) issue(kt + STAGES - 1);
-    const uint8_t* As = sA + (kt % STAGES) * S::A_STAGE;
-    const uint8_t* Bs = sB + (kt % STAGES) * S::B_STAGE;
-    const uint8_t* Ss = sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2;
-    // All LDS reads of the stage first (the reads of ks = 1 overlap the
-    // MFMAs of ks = 0), then per ks: decode every weight fragment, then the
-    // FM x FN MFMAs back to back.  Logical chunk ks*4 + grp of an A row sits
-    // at physical chunk (grp ^ sw) ^ (ks*4): flipping bit 6 of the byte
-    // offset selects the ks = 1 half.
-    V8 af[2][FM];
-    uint32_t raw[2][FN];
-    uint32_t sb[2][FN];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-        af[ks][fm] = *reinterpret_cast<const V8*>(As + ((a_rd0 + fm * 16 * 128) ^ (ks * 64)));
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        raw[ks][fn] =
-            *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 16 * 32 + ((ks ^ b_sw) * 16));
-        sb[ks][fn] = Ss[s_rd + fn * 16 * 4 + ks];
-      }
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      V8 bf[FN];
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) bf[fn] = Decode<T>::run(raw[ks][fn], e8m0_scale(sb[ks][fn]));
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) acc[fm][fn] = mfma16(bf[fn], af[ks][fm], acc[fm][fn]);
-    }
+    stage_math<T, FM, FN>(sA + (kt % STAGES) * S::A_STAGE, sB + (kt % STAGES) * S::B_STAGE,
+                          sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2, a_rd0, b_rd,
+                          b_sw, s_rd, acc);
   }
 
   // ---- epilogue: lane owns row wm*FM*16 + fm*16 + c16 and columns
@@ -296,6 +302,25 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   // a K slice's partial sums are stored raw; scaling and bias come once,
   // after the slices are summed
   const float alpha = (EPI == EPI_PARTIAL) ? 1.0f : scalar_alpha(g, expert);
+  // the lane's bias values, once (columns past N read as zero)
+  float bv[EPI == EPI_STORE ? FN : 1][4];
+  if (EPI == EPI_STORE && g.bias) {
+#pragma unroll
+    for (int fn = 0; fn < (EPI == EPI_STORE ? FN : 1); ++fn) {
+      const int col = ncol0 + wn * FN * 16 + fn * 16 + grp * 4;
+      const T* bp = static_cast<const T*>(g.bias) + col;
+      if (col + 4 <= g.n && (reinterpret_cast<uintptr_t>(bp) & 7) == 0) {
+        const uint2 v = *reinterpret_cast<const uint2*>(bp);
+        bv[fn][0] = to_f32(__builtin_bit_cast(T, (uint16_t)(v.x & 0xFFFF)));
+        bv[fn][1] = to_f32(__builtin_bit_cast(T, (uint16_t)(v.x >> 16)));
+        bv[fn][2] = to_f32(__builtin_bit_cast(T, (uint16_t)(v.y & 0xFFFF)));
+        bv[fn][3] = to_f32(__builtin_bit_cast(T, (uint16_t)(v.y >> 16)));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bv[fn][i] = col + i < g.n ? to_f32(bp[i]) : 0.f;
+      }
+    }
+  }
 #pragma unroll
   for (int pass = 0; pass < EPI_PASSES; ++pass) {
     {
@@ -340,10 +365,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] = acc[fm][fn][i] * alpha * rw;
             if (g.bias) {
-              const T* bp = static_cast<const T*>(g.bias) + ncol0 + tcol;
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                if (ncol0 + tcol + i < g.n) o[i] += to_f32(bp[i]);
+              for (int i = 0; i < 4; ++i) o[i] += bv[fn][i];
             }
             *reinterpret_cast<uint2*>(crow + tcol * 2) =
                 uint2{pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3])};
@@ -380,6 +403,346 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   }
 }
 
+// ---------------------------------------------------------------- persistent
+// Grids of several rounds (more tiles than resident workgroups) pay a fixed
+// cost per tile in the kernel above: the first stage's load latency, the
+// epilogue and the workgroup turnover, all exposed because the resident
+// workgroups run in step.  At K = 768 (a MoE down projection) that is ~20%
+// of a tile.  w4a16_pp keeps one workgroup per slot and walks tiles t =
+// blockIdx.x, + gridDim.x, ... (gridDim.x a multiple of 8, so every tile
+// stays on the XCD that tile_of assigns it).  The stage counter runs on
+// across tiles: the last stage of a tile issues the first stage of the next
+// one into the free buffer, so the pipeline never drains.  The epilogue
+// writes 4 outputs per lane straight from the accumulators (8-byte buffer
+// stores; no LDS staging, which would need room beside the stage buffers).
+// Per-row metadata goes through two LDS tables (this tile, next tile): the
+// next tile's sorted ids are loaded during the current tile's first stage
+// and turned into output / activation rows at its last one; route weights
+// and bias are loaded during the tile's own first stage.  Same MFMA order
+// and epilogue arithmetic as w4a16_pf: results are bitwise equal.
+// Requirements (host): the w4a16_pf ones, 2 stages, 1 x 4 waves, output
+// columns and row stride multiples of 4, 8-byte aligned output and output
+// rows below 2 GiB.
+
+extern "C" __device__ void llvm_amdgcn_raw_buffer_store_v2i32(i32x2 vdata, i32x4 rsrc,
+                                                              uint32_t voffset, int soffset,
+                                                              int aux)
+    __asm("llvm.amdgcn.raw.buffer.store.v2i32");
+
+template <typename T, int FM, int FN, int EPI, int MINB>
+__global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int nbn,
+                                                      uint32_t c_bytes) {
+  typedef PfShape<1, 4, FM, FN, 2> S;
+  constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
+  constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
+  constexpr int BIAS_PER = (OUT_COLS + NT - 1) / NT;
+  // table slot: output row, activation row (-1: none), route weight per
+  // tile row; bias per output column
+  constexpr int TAB = BM * 12 + OUT_COLS * 4;
+  static_assert(EPI == EPI_STORE || EPI == EPI_SILU_MUL, "plain or SiLU epilogue");
+  static_assert(EPI != EPI_SILU_MUL || FN % 2 == 0, "SiLU pairs need even FN");
+  static_assert(BM <= NT, "one table row per thread");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[S::PIPE + 2 * TAB];
+  uint8_t* const sA = smem;
+  uint8_t* const sB = smem + 2 * S::A_STAGE;
+  uint8_t* const sS = smem + 2 * (S::A_STAGE + S::B_STAGE);
+  uint8_t* const sT = smem + S::PIPE;
+  auto t_orow = [&](int slot) { return reinterpret_cast<int*>(sT + slot * TAB); };
+  auto t_arow = [&](int slot) { return reinterpret_cast<int*>(sT + slot * TAB + BM * 4); };
+  auto t_rw = [&](int slot) { return reinterpret_cast<float*>(sT + slot * TAB + BM * 8); };
+  auto t_bias = [&](int slot) { return reinterpret_cast<float*>(sT + slot * TAB + BM * 12); };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = wn (one wave row)
+  const int c16 = lane & 15;
+  const int grp = lane >> 4;
+  const int ntile = nbm * nbn;
+  const int nk = g.k / 64;
+  const int64_t b_rows_total = (EPI == EPI_SILU_MUL) ? 2 * (int64_t)g.inter : (int64_t)g.n;
+
+  // sorted id (or dense row) of row `tid` of the tile at row block bm_ ->
+  // output row and activation row, -1 when the row is padding
+  auto rows_of = [&](int bm_, int sid, int& orow, int& arow) {
+    const int64_t pos = (int64_t)bm_ * BM + tid;
+    if (g.sorted_ids == nullptr) {
+      orow = pos < g.m ? (int)pos : -1;
+      arow = orow;
+    } else {
+      const bool ok = sid >= 0 && sid < g.num_valid;
+      orow = ok ? sid : -1;
+      arow = ok ? sid / g.top_k : -1;
+    }
+  };
+
+  int t = blockIdx.x, bm, bn;
+  if (!tile_of(g, BM, nbm, nbn, bm, bn, t, ntile)) return;
+  int expert = g.sorted_ids ? block_expert(g, (int64_t)bm * BM) : 0;
+  if (tid < BM) {
+    const int sid = g.sorted_ids ? g.sorted_ids[(int64_t)bm * BM + tid] : 0;
+    int o, a;
+    rows_of(bm, sid, o, a);
+    t_orow(0)[tid] = o;
+    t_arow(0)[tid] = a;
+  }
+  __syncthreads();
+
+  // ---- load offsets and buffer resources of a tile (its rows in table
+  // `slot`); stage kt adds kt * stride as the instruction's scalar offset
+  uint32_t a_off[S::A_PER], b_off[S::B_PER], s_off[S::S_PER];
+  i32x4 rA = make_rsrc(g.a, (uint32_t)(g.a_rows * g.lda * (int64_t)sizeof(T)));
+  i32x4 rB, rS;
+  auto setup = [&](int bn_, int expert_, int slot) {
+    const int ncol0_ = bn_ * OUT_COLS;
+    const int e = expert_ < 0 ? 0 : expert_;
+    // expert < 0: empty resources, every operand reads zero
+    rB = make_rsrc(g.b + e * g.b_e, expert_ < 0 ? 0u : (uint32_t)(b_rows_total * g.b_n));
+    rS = make_rsrc(g.bs + e * g.bs_e, expert_ < 0 ? 0u : (uint32_t)(b_rows_total * g.bs_n));
+    auto weight_row = [&](int i) -> int {
+      int orow, grow;
+      if (EPI == EPI_SILU_MUL) {
+        const int cbk = i >> 4;
+        orow = ncol0_ + (cbk >> 1) * 16 + (i & 15);
+        grow = (cbk & 1 ? g.inter : 0) + orow;
+      } else {
+        orow = ncol0_ + i;
+        grow = orow;
+      }
+      return orow < g.n ? grow : -1;
+    };
+#pragma unroll
+    for (int j = 0; j < S::A_PER; ++j) {
+      const int q = j * S::NW + wave;
+      const int row = q * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ (row & 7);
+      const int ar = q < S::A_TOT ? t_arow(slot)[row] : -1;
+      a_off[j] = (ar >= 0 && expert_ >= 0) ? (uint32_t)(ar * g.lda * (int64_t)sizeof(T)) + c * 16
+                                           : kOOB;
+    }
+#pragma unroll
+    for (int j = 0; j < S::B_PER; ++j) {
+      const int q = j * S::NW + wave;
+      const int row = q * 32 + (lane >> 1);
+      const int c = (lane & 1) ^ ((row >> 3) & 1);
+      const int grow = q < S::B_TOT ? weight_row(row) : -1;
+      b_off[j] = grow >= 0 ? (uint32_t)(grow * g.b_n) + c * 16 : kOOB;
+    }
+#pragma unroll
+    for (int j = 0; j < S::S_PER; ++j) {
+      const int q = j * S::NW + wave;
+      const int grow = q < S::S_TOT ? weight_row(q * 64 + lane) : -1;
+      s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
+    }
+  };
+  // stage kt of the current tile into buffer gk % 2 (gk: stage counter
+  // across tiles; every tile has an even number of stages, so gk and kt
+  // have the same parity and the scale slots alternate as in w4a16_pf)
+  auto issue = [&](int kt, int gk) {
+    const int st = gk & 1;
+    if ((kt & 1) == 0) {
+#pragma unroll
+      for (int j = 0; j < S::S_PER; ++j) {
+        const int q = j * S::NW + wave;
+        if (q < S::S_TOT)
+          llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + ((gk >> 1) & 1) * S::S_SLOT + q * 256),
+                                          4, (int)s_off[j], (kt >> 1) * 4, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < S::A_PER; ++j) {
+      const int q = j * S::NW + wave;
+      if (S::A_TOT % S::NW == 0 || q < S::A_TOT)
+        llvm_amdgcn_raw_buffer_load_lds(rA, lds_ptr(sA + st * S::A_STAGE + q * 1024), 16,
+                                        (int)a_off[j], kt * 128, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < S::B_PER; ++j) {
+      const int q = j * S::NW + wave;
+      if (S::B_TOT % S::NW == 0 || q < S::B_TOT)
+        llvm_amdgcn_raw_buffer_load_lds(rB, lds_ptr(sB + st * S::B_STAGE + q * 1024), 16,
+                                        (int)b_off[j], kt * 32, 0, 0);
+    }
+  };
+
+  const int a_rd0 = c16 * 128 + ((grp ^ (c16 & 7)) * 16);
+  const int b_sw = (c16 >> 3) & 1;
+  const int b_rd = (wave * FN * 16 + c16) * 32 + grp * 4;
+  const int s_rd = (wave * FN * 16 + c16) * 4;
+  const i32x4 rC = make_rsrc(g.c, c_bytes);
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  setup(bn, expert, 0);
+  int gk = 0;
+  issue(0, 0);
+  for (int slot = 0;; slot ^= 1) {
+    const int tn = t + (int)gridDim.x;
+    int bm_n = 0, bn_n = 0;
+    const bool has_next = tn < ntile && tile_of(g, BM, nbm, nbn, bm_n, bn_n, tn, ntile);
+    const int expert_n = (has_next && g.sorted_ids) ? block_expert(g, (int64_t)bm_n * BM) : 0;
+    const int ncol0 = bn * OUT_COLS;
+    int sid_n = 0;     // next tile: sorted id of row tid
+    float rwv = 1.0f;  // this tile: route weight of row tid
+    float biasv[BIAS_PER];
+#pragma unroll
+    for (int i = 0; i < BIAS_PER; ++i) biasv[i] = 0.f;
+    // stage gk of the tile's buffer pair -> MFMAs
+    auto math = [&]() {
+      stage_math<T, FM, FN>(sA + (gk & 1) * S::A_STAGE, sB + (gk & 1) * S::B_STAGE,
+                            sS + ((gk >> 1) & 1) * S::S_SLOT + (gk & 1) * 2, a_rd0, b_rd, b_sw,
+                            s_rd, acc);
+    };
+    // Every stage: wait until stage gk has landed (nothing later is in
+    // flight), then a barrier publishes it and retires the reads of the
+    // buffer the next issue overwrites.  The first and last stages are
+    // peeled off so that the loop in between is the plain pipeline.
+    // -- first stage: also the metadata loads consumed at the last one
+    wait_vmcnt<0>();
+    barrier_only();
+    issue(1, gk + 1);
+    if (tid < BM) {
+      if (has_next && g.sorted_ids) sid_n = g.sorted_ids[(int64_t)bm_n * BM + tid];
+      if (EPI == EPI_STORE && g.route_w) {
+        const int o = t_orow(slot)[tid];
+        rwv = o >= 0 ? g.route_w[o] : 0.f;
+      }
+    }
+    if (EPI == EPI_STORE && g.bias) {
+#pragma unroll
+      for (int i = 0; i < BIAS_PER; ++i) {
+        const int col = ncol0 + tid + i * NT;
+        if (tid + i * NT < OUT_COLS && col < g.n)
+          biasv[i] = to_f32(static_cast<const T*>(g.bias)[col]);
+      }
+    }
+    // keep the fragment reads below the extra code (register pressure)
+    __builtin_amdgcn_sched_barrier(0);
+    math();
+    ++gk;
+    // -- stages 1 .. nk - 2
+    for (int kt = 1; kt < nk - 1; ++kt, ++gk) {
+      wait_vmcnt<0>();
+      barrier_only();
+      issue(kt + 1, gk + 1);
+      math();
+    }
+    // -- last stage: tables (this tile's route weights and bias for its
+    // epilogue, the next tile's rows for its loads), then the next tile's
+    // first stage into the free buffer
+    wait_vmcnt<0>();
+    if (tid < BM) {
+      t_rw(slot)[tid] = rwv;
+      if (has_next) {
+        int o, a;
+        rows_of(bm_n, sid_n, o, a);
+        t_orow(slot ^ 1)[tid] = o;
+        t_arow(slot ^ 1)[tid] = a;
+      }
+    }
+    if (EPI == EPI_STORE && g.bias) {
+#pragma unroll
+      for (int i = 0; i < BIAS_PER; ++i)
+        if (tid + i * NT < OUT_COLS) t_bias(slot)[tid + i * NT] = biasv[i];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    barrier_only();
+    if (has_next) {
+      setup(bn_n, expert_n, slot ^ 1);
+      issue(0, gk + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    math();
+    ++gk;
+
+    // ---- epilogue: lane holds rows fm*16 + c16, columns fn*16 + grp*4 ..
+    // +3 of the wave's 16-column blocks; expert < 0 (not on this device)
+    // writes zeros (aiter:156-172)
+    const float alpha = expert >= 0 ? scalar_alpha(g, expert) : 0.f;
+    // table reads first: the compiler does not move LDS reads across the
+    // buffer stores
+    uint32_t base[FM];
+    float rw[FM];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int orow = t_orow(slot)[fm * 16 + c16];
+      base[fm] = orow >= 0 ? (uint32_t)(orow * g.ldc * (int64_t)sizeof(T)) : kOOB;
+      rw[fm] = (EPI == EPI_STORE && g.route_w) ? t_rw(slot)[fm * 16 + c16] : 1.0f;
+    }
+    float bv[EPI == EPI_STORE ? FN : 1][4];
+    if (EPI == EPI_STORE) {
+#pragma unroll
+      for (int fn = 0; fn < (EPI == EPI_STORE ? FN : 1); ++fn)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          bv[fn][i] = g.bias ? t_bias(slot)[wave * FN * 16 + fn * 16 + grp * 4 + i] : 0.f;
+    }
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      if (EPI == EPI_SILU_MUL) {
+#pragma unroll
+        for (int fn = 0; fn < FN; fn += 2) {
+          const int col = ncol0 + ((wave * FN + fn) >> 1) * 16 + grp * 4;
+          float h[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // vllm:249-252 on tensors of T (as in w4a16_pf)
+            const T gb = from_f32<T>(acc[fm][fn][i] * alpha);
+            const T ub = from_f32<T>(acc[fm][fn + 1][i] * alpha);
+            const T sb = from_f32<T>(silu_f32(to_f32(gb)));
+            h[i] = expert >= 0 ? to_f32(sb) * to_f32(ub) : 0.f;
+          }
+          const uint32_t off =
+              (base[fm] != kOOB && col < g.n) ? base[fm] + col * (int)sizeof(T) : kOOB;
+          llvm_amdgcn_raw_buffer_store_v2i32(
+              i32x2{(int)pack2<T>(h[0], h[1]), (int)pack2<T>(h[2], h[3])}, rC, off, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int col = ncol0 + wave * FN * 16 + fn * 16 + grp * 4;
+          float o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            o[i] = acc[fm][fn][i] * alpha * rw[fm];
+            if (g.bias) o[i] += bv[fn < (EPI == EPI_STORE ? FN : 1) ? fn : 0][i];
+            if (expert < 0) o[i] = 0.f;
+          }
+          const uint32_t off =
+              (base[fm] != kOOB && col < g.n) ? base[fm] + col * (int)sizeof(T) : kOOB;
+          llvm_amdgcn_raw_buffer_store_v2i32(
+              i32x2{(int)pack2<T>(o[0], o[1]), (int)pack2<T>(o[2], o[3])}, rC, off, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (!has_next) break;
+    t = tn;
+    bm = bm_n;
+    bn = bn_n;
+    expert = expert_n;
+  }
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB>
 int launch_cfg(const GemmArgs& g, hipStream_t st) {
   typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
@@ -392,6 +755,26 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
   if (nwg <= 0 || nwg > 0x7FFFFFFF) {
     set_error("w4a16 prefill: bad grid");
     return MXFP4_ERR_VALUE;
+  }
+  if constexpr (EPI != EPI_PARTIAL && WGM == 1 && WGN == 4 && STAGES == 2 && FN <= 4) {
+    // routed grid of more tiles than resident workgroups: the persistent
+    // kernel (dense grids run 2-5% slower in it: their tiles start with
+    // one load round trip, not the routed two, and gain nothing)
+    const int64_t c_bytes = g.num_valid * g.ldc * (int64_t)sizeof(T);
+    if (g.sorted_ids && g.n % 4 == 0 && g.ldc % 4 == 0 && c_bytes < (int64_t)0x7FFFFFFF) {
+      auto kern = w4a16_pp<T, FM, FN, EPI, MINB>;
+      static int per_cu = -1;  // same on every device of the build target
+      if (per_cu < 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, S::NT, 0) != hipSuccess) nb = 0;
+        per_cu = nb;
+      }
+      const int64_t slots = ((int64_t)per_cu * device_cus()) & ~(int64_t)7;
+      if (slots >= 8 && nwg > slots) {
+        kern<<<(unsigned)slots, S::NT, 0, st>>>(g, (int)nbm, nbn, (uint32_t)c_bytes);
+        return launch_status("w4a16 persistent prefill launch");
+      }
+    }
   }
   w4a16_pf<T, WGM, WGN, FM, FN, STAGES, EPI, MINB><<<(unsigned)nwg, S::NT, 0, st>>>(g, (int)nbm,
                                                                                     nbn);

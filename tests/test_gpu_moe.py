@@ -308,6 +308,21 @@ def test_moe_layer_small_vs_golden_and_safe():
     assert_layer_parity(y, g["layer_y"], safe)
 
 
+def _fp16_layer_oracle(xs, w13, s13, w2, s2, w, ids):
+    """The MoE layer in float64 with the fp16 rounding points of the
+    reference composition (gate_up, silu, product, down; FP32-exact sum)."""
+    m, top_k = ids.shape
+    ones = np.ones(w13.shape[0])
+    gu = O.round_to_dtype(O.fused_moe_fp64(xs, w13, s13, 1.0, ones, w, ids, False,
+                                           compute_dtype="f16"), "f16")
+    inter = gu.shape[-1] // 2
+    gg, uu = gu[..., :inter], gu[..., inter:]
+    h = O.round_to_dtype(O.round_to_dtype(gg / (1 + np.exp(-gg)), "f16") * uu, "f16")
+    d = O.fused_moe_fp64(h.reshape(m * top_k, inter), w2, s2, 1.0, ones, w.reshape(-1, 1),
+                         ids.reshape(-1, 1), True, compute_dtype="f16")
+    return O.round_to_dtype(d, "f16")[:, 0].reshape(m, top_k, -1).sum(1)
+
+
 def test_moe_layer_fp16_and_invalid_ids():
     rng = np.random.default_rng(5)
     # small scales keep every fp16 intermediate finite
@@ -320,17 +335,60 @@ def test_moe_layer_fp16_and_invalid_ids():
     ids[5, 0] = -1
     y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
     assert y.dtype == torch.float16
-    xs = x.float().numpy()
-    # fp16 layer oracle: the same composition with fp16 rounding points
-    ones = np.ones(8)
-    gu = O.round_to_dtype(O.fused_moe_fp64(xs, w13, s13, 1.0, ones, w.numpy(), ids.numpy(), False,
-                                           compute_dtype="f16"), "f16")
-    inter = gu.shape[-1] // 2
-    gg, uu = gu[..., :inter], gu[..., inter:]
-    h = O.round_to_dtype(O.round_to_dtype(gg / (1 + np.exp(-gg)), "f16") * uu, "f16")
-    d = O.fused_moe_fp64(h.reshape(m * 2, inter), w2, s2, 1.0, ones, w.numpy().reshape(-1, 1),
-                         ids.numpy().reshape(-1, 1), True, compute_dtype="f16")
-    oracle = O.round_to_dtype(d, "f16")[:, 0].reshape(m, 2, -1).sum(1)
+    oracle = _fp16_layer_oracle(x.float().numpy(), w13, s13, w2, s2, w.numpy(), ids.numpy())
     t = torch.from_numpy
     safe = O.moe_layer_safe(x, t(w13), t(s13), t(w2), t(s2), w, ids)
     assert_layer_parity(y, oracle, safe)
+
+
+def test_moe_layer_fp16_multi_round_grid():
+    # fp16 layer with ~90 routed 128-row blocks: both GEMMs have more tiles
+    # than resident workgroups (the persistent kernel, SiLU and plain
+    # epilogues); sampled rows against the fp16-rounded oracle
+    rng = np.random.default_rng(2600)
+    e, hidden, inter, top_k, m = 8, 2048, 768, 4, 2600
+    w13, s13 = rand_mxfp4(rng, (e, 2 * inter), hidden, lo=116, hi=121)
+    w2, s2 = rand_mxfp4(rng, (e, hidden), inter, lo=116, hi=121)
+    x = rand_act(2601, (m, hidden), torch.float16)
+    w, ids = _route(m, e, top_k, 2602)
+    ids[17, 2] = -1  # dropped: contributes nothing
+    y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
+    rows = np.sort(np.concatenate([[17], np.random.default_rng(9).choice(m, 47, False)]))
+    rows = np.unique(rows)
+    oracle = _fp16_layer_oracle(x.float().numpy()[rows], w13, s13, w2, s2, w.numpy()[rows],
+                                ids.numpy()[rows])
+    t = torch.from_numpy
+    safe = O.moe_layer_safe(x[rows], t(w13), t(s13), t(w2), t(s2), w[rows], ids[rows])
+    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="fp16 layer, several rounds")
+
+
+@pytest.mark.parametrize("n,dtype", [(3072, torch.bfloat16), (2048, torch.float16)])
+def test_routed_gemm_multi_round_grid(n, dtype):
+    # ~70 routed 128-row blocks x 12-16 column tiles: more tiles than
+    # resident workgroups (the persistent kernel).  Expert -1 blocks, ids
+    # outside [0, E) (rows left untouched), route weights, per-expert scales
+    rng = np.random.default_rng(n)
+    m, k, e, top_k, block_m = 2048, 256, 8, 4, 128
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(n + 1, (m, k), dtype)
+    w, ids = _route(m, e, top_k, n + 2)
+    dropped = ((5, 1), (77, 0), (1000, 3))
+    ids[5, 1], ids[77, 0], ids[1000, 3] = -1, e, e + 3
+    srt, exp_, npp = O.make_routing(ids.numpy(), block_m=block_m, num_experts=e)
+    exp_ = exp_.copy()
+    exp_[exp_ == 6] = -1
+    C = torch.full((m, top_k, n), 3.0, dtype=dtype, device="cuda")
+    mx.fused_moe_mxfp4(cuda(a), cuda(wp), C, torch.tensor([0.5], device="cuda"),
+                       torch.linspace(1, 2, e, device="cuda"), None, cuda(ws), cuda(w), cuda(ids),
+                       cuda(srt), cuda(exp_), cuda(npp), True, top_k, False, False,
+                       {"BLOCK_SIZE_M": block_m}, dtype)
+    ids_np = ids.numpy()
+    dt = "f16" if dtype == torch.float16 else "bf16"
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 0.5, np.linspace(1, 2, e), w.numpy(),
+                              ids_np, True, compute_dtype=dt)
+    oracle[ids_np == 6] = 0.0  # expert -1 blocks write zeros
+    out = C.float().cpu().numpy()
+    for t_, s_ in dropped:
+        assert np.all(out[t_, s_] == 3.0)
+        oracle[t_, s_] = 3.0
+    assert_parity(out, oracle, what=f"n={n} {dtype}")
