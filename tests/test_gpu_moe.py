@@ -362,13 +362,14 @@ def test_moe_layer_fp16_multi_round_grid():
     assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="fp16 layer, several rounds")
 
 
-@pytest.mark.parametrize("n,dtype", [(3072, torch.bfloat16), (2048, torch.float16)])
-def test_routed_gemm_multi_round_grid(n, dtype):
-    # ~70 routed 128-row blocks x 12-16 column tiles: more tiles than
-    # resident workgroups (the persistent kernel).  Expert -1 blocks, ids
-    # outside [0, E) (rows left untouched), route weights, per-expert scales
+@pytest.mark.parametrize("m,n,dtype", [(2300, 3072, torch.float16), (2048, 2048, torch.bfloat16)])
+def test_routed_gemm_multi_round_grid(m, n, dtype):
+    # 68-75 routed 128-row blocks: more tiles than resident workgroups (the
+    # persistent kernel; 128 x 256 tiles at N = 3072, whose rounds are 88%
+    # full, 128 x 128 at N = 2048).  Expert -1 blocks, ids outside [0, E)
+    # (rows left untouched), route weights, per-expert scales
     rng = np.random.default_rng(n)
-    m, k, e, top_k, block_m = 2048, 256, 8, 4, 128
+    k, e, top_k, block_m = 256, 8, 4, 128
     wp, ws = rand_mxfp4(rng, (e, n), k)
     a = rand_act(n + 1, (m, k), dtype)
     w, ids = _route(m, e, top_k, n + 2)
