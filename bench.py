@@ -348,6 +348,14 @@ def sweep(mx, torch, np):
     res["dequant_bf16_128x1536x2048"] = {"us": round(t * 1e3, 1), "GB/s": round(db / t / 1e6, 1),
                                          "hbm_frac": round(db / t / 1e6 / HBM_PEAK_GBS, 4)}
     log(f"dequant: {res['dequant_bf16_128x1536x2048']}")
+    # --- router: logits f32 [4096, 128] -> top-8 weights and ids
+    # (graph replays of 16 calls: the kernel is shorter than an eager call's
+    # Python overhead)
+    logits = torch.randn((4096, 128), generator=torch.Generator().manual_seed(12)).cuda()
+    t = time_graph([lambda: mx.route_topk(logits, 8)] * 16, replays=20)
+    rb = logits.numel() * 4 + 4096 * 8 * (4 + 8)
+    res["route_topk_4096x128_k8"] = {"us": round(t * 1e3, 2), "GB/s": round(rb / t / 1e6, 1)}
+    log(f"router: {res['route_topk_4096x128_k8']}")
     return res
 
 

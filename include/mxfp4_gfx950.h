@@ -133,6 +133,20 @@ int mxfp4_moe_align(const void* topk_ids, int ids_dtype, int64_t num_routes, int
                     void* stream);
 
 /*
+ * Router -- the topk_weights / topk_ids the MoE layer consumes (vllm:233-265),
+ * built as the reference tests build them (test:242-244: softmax over the
+ * experts, then torch.topk) and, with renormalize != 0, divided by their sum
+ * (the MoE benchmark configuration).  logits F32 [m, num_experts] (row
+ * stride in elements) -> topk_weights F32 [m, top_k] and topk_ids (I32 or
+ * I64) [m, top_k], contiguous; slot r holds the r-th most probable expert,
+ * ties to the lower expert id.  Logits must be finite.  num_experts <= 1024,
+ * 1 <= top_k <= min(num_experts, 64).
+ */
+int mxfp4_moe_route(const float* logits, int64_t m, int num_experts, int64_t row_stride,
+                    int top_k, int renormalize, float* topk_weights, void* topk_ids, int ids_dtype,
+                    void* stream);
+
+/*
  * Routed grouped GEMM -- the compute of fused_moe_mxfp4_soft, soft:379-494,
  * and of AITER's fused_moe_mxfp4, aiter:28-364.
  *   a: activations [a_rows, k]: BF16/F16/F32 (a_dtype), or packed u8

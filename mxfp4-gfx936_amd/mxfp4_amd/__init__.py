@@ -10,6 +10,7 @@ current stream; no host synchronisation, no fallback path):
 * ``fused_moe_mxfp4`` -- AITER's entry (integration/aiter/moe_op_mxfp4.py);
 * ``moe_layer`` / ``make_routing`` -- the vLLM MoE layer and routing
   metadata (integration/vllm/vllm_mxfp4_gfx936.py:119-146, 233-265);
+  ``route_topk`` -- router logits -> the layer's top-k weights and ids;
 * ``dynamic_mxfp4_quant`` / ``linear_mxfp4_w4a4`` -- activation quantizer
   and dense W4A4 on the block-scaled FP4 MFMA.
 
@@ -25,7 +26,7 @@ from .moe_op_mxfp4_soft import (  # noqa: F401
     make_routing_device,
 )
 from .moe_op_mxfp4 import fused_moe_mxfp4  # noqa: F401
-from .moe_layer import make_routing, moe_layer  # noqa: F401
+from .moe_layer import make_routing, moe_layer, route_topk  # noqa: F401
 from .quant import dynamic_mxfp4_quant, linear_mxfp4_w4a4  # noqa: F401
 from . import _lib  # noqa: F401
 
@@ -36,6 +37,7 @@ __all__ = [
     "fused_moe_mxfp4",
     "moe_layer",
     "make_routing",
+    "route_topk",
     "make_routing_device",
     "dynamic_mxfp4_quant",
     "linear_mxfp4_w4a4",

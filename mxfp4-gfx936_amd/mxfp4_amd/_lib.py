@@ -46,6 +46,7 @@ SIGNATURES = {
     "mxfp4_linear_w4a4": [_P, _P, _I64, _I64, _P, _P, _I64, _P, _I, _P],
     "mxfp4_moe_align_sizes": [_I64, _I, _I, _P, _P, _P],
     "mxfp4_moe_align": [_P, _I, _I64, _I, _I, _P, _P, _P, _P, _I64, _P],
+    "mxfp4_moe_route": [_P, _I64, _I, _I64, _I, _I, _P, _P, _I, _P],
     "mxfp4_moe_gemm": [_P, _I, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I, _I64, _P, _P,
                        _P, _I, _P, _P, _P, _I64, _I, _I64, _I, _P],
     "mxfp4_moe_layer_workspace_size": [_I64, _I, _I, _I64, _I64, _P],

@@ -15,7 +15,8 @@ of vllm:119-146), the gate_up grouped GEMM with SiLU*mul fused into its
 epilogue (rounding g, u, silu(g) and the product to x.dtype as the reference
 does), the down grouped GEMM with the route weight fused into its epilogue,
 and a deterministic FP32 top-k combine.  ``make_routing`` exposes the routing
-metadata in the reference format.
+metadata in the reference format; ``route_topk`` computes the layer's
+``topk_weights`` / ``topk_ids`` from router logits on the device.
 """
 
 from __future__ import annotations
@@ -104,3 +105,38 @@ def make_routing(topk_ids: torch.Tensor, block_m: int = 64, num_experts: int | N
     if num_experts is None:
         num_experts = int(topk_ids.max().item()) + 1 if topk_ids.numel() else 1
     return make_routing_device(topk_ids, num_experts, block_m)
+
+
+def route_topk(router_logits: torch.Tensor, top_k: int, renormalize: bool = True,
+               ids_dtype: torch.dtype = torch.int64):
+    """Router logits -> (topk_weights, topk_ids) on the device, the inputs of
+    ``moe_layer`` (vllm:233-265): softmax over the experts, top-k (as the
+    reference tests build them, test:242-244), then, with ``renormalize``,
+    weights divided by their sum.  ``router_logits`` [..., E] (converted to
+    float32) -> float32 and ``ids_dtype`` (int64 as ``torch.topk``, or int32)
+    tensors [..., top_k]; slot r holds the r-th most probable expert, ties
+    to the lower expert id.  Logits must be finite; E <= 1024,
+    top_k <= min(E, 64)."""
+    if ids_dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"topk_ids dtype must be int32 or int64, got {ids_dtype}")
+    if router_logits.dim() < 1:
+        raise ValueError("router_logits needs an expert dimension")
+    num_experts = router_logits.shape[-1]
+    if not 1 <= top_k <= min(num_experts, 64) or num_experts > 1024:
+        raise ValueError(f"unsupported top_k {top_k} for {num_experts} experts")
+    device = _lib.require_device(router_logits)
+    lead = router_logits.shape[:-1]
+    logits = router_logits.reshape(-1, num_experts).to(torch.float32)
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    m = logits.shape[0]
+    weights = torch.empty((*lead, top_k), dtype=torch.float32, device=device)
+    ids = torch.empty((*lead, top_k), dtype=ids_dtype, device=device)
+    if m == 0:
+        return weights, ids
+    lib = _lib.load()
+    with _lib.on_device(device):
+        _lib.check(lib.mxfp4_moe_route(
+            _lib.ptr(logits), m, num_experts, logits.stride(0), top_k, int(bool(renormalize)),
+            _lib.ptr(weights), _lib.ptr(ids), _lib.dtype_code(ids_dtype), _lib.stream_of(device)))
+    return weights, ids

@@ -300,6 +300,28 @@ def make_routing(topk_ids: np.ndarray, block_m: int = 64, num_experts: int | Non
     return sorted_ids, expert_ids, np.array([sorted_ids.size], dtype=np.int32)
 
 
+def route_topk_fp64(logits: np.ndarray, top_k: int, renormalize: bool = True):
+    """Router: softmax over the experts, top-k, optional renormalisation, in
+    float64 -- the ``topk_weights`` / ``topk_ids`` the MoE layer consumes
+    (vllm:233-265), built as test:242-244 builds them (softmax, then
+    ``torch.topk``) and, with ``renormalize``, divided by their sum.  Slots
+    in descending probability; ties to the lower expert id (``torch.topk``
+    leaves tie order unspecified).  Returns (weights float64, ids int64)."""
+    x = np.asarray(logits, dtype=np.float64)
+    ne = x.shape[-1]
+    flat = x.reshape(-1, ne)
+    # descending logit, then ascending expert id
+    order = np.lexsort((np.broadcast_to(np.arange(ne), flat.shape), -flat), axis=-1)
+    ids = order[:, :top_k]
+    p = np.exp(flat - flat.max(-1, keepdims=True))
+    p = p / p.sum(-1, keepdims=True)
+    w = np.take_along_axis(p, ids, -1)
+    if renormalize:
+        w = w / w.sum(-1, keepdims=True)
+    shape = x.shape[:-1] + (top_k,)
+    return w.reshape(shape), ids.astype(np.int64).reshape(shape)
+
+
 # ----------------------------------------------------------------------------
 # FP64 oracles
 # ----------------------------------------------------------------------------

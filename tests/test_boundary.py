@@ -238,3 +238,22 @@ def test_moe_layer_and_quant_validation():
         mx.dynamic_mxfp4_quant(x, mode="floor")
     with pytest.raises(ValueError, match="divisible by 32"):
         mx.dynamic_mxfp4_quant(x[:, :40])
+
+
+def test_route_topk_argument_errors():
+    # the router's argument checks run before anything touches a device
+    x = torch.zeros(4, 8)
+    with pytest.raises(TypeError):
+        mx.route_topk(x, 2, ids_dtype=torch.int16)
+    with pytest.raises(ValueError):
+        mx.route_topk(x, 9)
+    with pytest.raises(ValueError):
+        mx.route_topk(torch.zeros(4, 2000), 2)
+    lib = _lib.load()
+    i64, f32 = _lib.dtype_code(torch.int64), _lib.dtype_code(torch.float32)
+    # C ABI: ids must be int32/int64, row stride >= experts, top_k <= experts
+    assert lib.mxfp4_moe_route(None, 4, 8, 8, 2, 1, None, None, f32, None) == _lib.ERR_TYPE
+    assert lib.mxfp4_moe_route(None, 4, 8, 4, 2, 1, None, None, i64, None) == _lib.ERR_VALUE
+    assert lib.mxfp4_moe_route(None, 4, 8, 8, 9, 1, None, None, i64, None) == _lib.ERR_VALUE
+    assert lib.mxfp4_moe_route(None, 4, 2048, 2048, 2, 1, None, None, i64, None) == _lib.ERR_VALUE
+    assert lib.mxfp4_moe_route(None, 0, 8, 8, 2, 1, None, None, i64, None) == _lib.OK

@@ -393,3 +393,56 @@ def test_routed_gemm_multi_round_grid(m, n, dtype):
         assert np.all(out[t_, s_] == 3.0)
         oracle[t_, s_] = 3.0
     assert_parity(out, oracle, what=f"n={n} {dtype}")
+
+
+# ---------------------------------------------------------------- router
+
+@pytest.mark.parametrize("m,e,top_k,renorm,ids_dtype",
+                         [(1, 128, 8, True, torch.int64), (4096, 128, 8, True, torch.int32),
+                          (333, 60, 4, False, torch.int64), (17, 1024, 16, True, torch.int64),
+                          (8, 7, 7, False, torch.int32), (100, 256, 64, True, torch.int64),
+                          (5, 65, 1, True, torch.int32)])
+def test_route_topk_matches_oracle(m, e, top_k, renorm, ids_dtype):
+    g = torch.Generator().manual_seed(m * 31 + e)
+    logits = torch.randn((m, e), generator=g) * 2.0
+    w, ids = mx.route_topk(cuda(logits), top_k, renormalize=renorm, ids_dtype=ids_dtype)
+    assert w.dtype == torch.float32 and ids.dtype == ids_dtype and w.shape == (m, top_k)
+    ow, oids = O.route_topk_fp64(logits.numpy(), top_k, renormalize=renorm)
+    assert np.array_equal(ids.cpu().numpy(), oids)
+    np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=2e-6, atol=0)
+
+
+def test_route_topk_strided_3d_and_ties():
+    # a [2, 9, E] view with a row stride past E; rows with tied logits pick
+    # the lower expert id first
+    g = torch.Generator().manual_seed(5)
+    base = torch.randn((2, 9, 200), generator=g)
+    logits = base[..., 10:138]  # 128 experts, row stride 200
+    logits[0, 3, :] = 0.0
+    logits[1, 4, [5, 77, 100]] = 9.0
+    w, ids = mx.route_topk(cuda(base)[..., 10:138], 4)
+    ow, oids = O.route_topk_fp64(logits.numpy(), 4)
+    assert w.shape == (2, 9, 4)
+    assert np.array_equal(ids.cpu().numpy(), oids)
+    assert ids[0, 3].tolist() == [0, 1, 2, 3] and ids[1, 4, :3].tolist() == [5, 77, 100]
+    np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=2e-6, atol=0)
+
+
+def test_route_topk_feeds_the_layer(layer_weights):
+    # the device router's output drives the MoE layer like torch's routing
+    w13, s13, w2, s2 = layer_weights
+    m = 64
+    x = rand_act(640, (m, 2048))
+    g = torch.Generator().manual_seed(641)
+    logits = torch.randn((m, 128), generator=g)
+    w, ids = mx.route_topk(cuda(logits), 8)
+    p = torch.softmax(logits, -1)
+    tw, tids = torch.topk(p, 8, -1)
+    tw = tw / tw.sum(-1, keepdim=True)
+    assert torch.equal(ids.cpu(), tids)
+    assert torch.allclose(w.cpu(), tw, rtol=2e-6, atol=0)
+    y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), w, ids)
+    oracle = O.moe_layer_fp64(x.float().numpy(), w13, s13, w2, s2, tw.numpy(), tids.numpy())
+    t = torch.from_numpy
+    safe = O.moe_layer_safe(x, t(w13), t(s13), t(w2), t(s2), tw, tids)
+    assert_layer_parity(y, oracle, safe, what="layer on device routing")

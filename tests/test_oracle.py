@@ -17,6 +17,7 @@ rule, a transposed operand -- fails at least one of them:
 
 from __future__ import annotations
 
+import math
 import os
 from fractions import Fraction
 
@@ -365,3 +366,30 @@ def test_parity_metric_floor():
     # the 1e-6 miss at a ~0 entry is judged against 1e-3 * rms, not 1e-9
     assert e["elem_rel"] < 1e-2
     assert O.parity_errors(o * 1.01, o)["elem_rel"] == pytest.approx(0.01)
+
+
+def test_router_oracle_pinned():
+    # test:242-244 through torch itself (float64 softmax, torch.topk), then
+    # the renormalisation; closed forms at two experts; ties by definition
+    import torch
+    rng = np.random.default_rng(242)
+    x = rng.standard_normal((64, 128))
+    p = torch.softmax(torch.from_numpy(x), dim=-1)
+    tw, ti = torch.topk(p, k=8, dim=-1)
+    w, ids = O.route_topk_fp64(x, 8, renormalize=False)
+    assert np.array_equal(ids, ti.numpy())
+    np.testing.assert_allclose(w, tw.numpy(), rtol=1e-13, atol=0)
+    wr, idr = O.route_topk_fp64(x, 8, renormalize=True)
+    assert np.array_equal(idr, ids)
+    np.testing.assert_allclose(wr, (tw / tw.sum(-1, keepdim=True)).numpy(), rtol=1e-13, atol=0)
+    # two experts: the larger logit wins with weight sigmoid(l0 - l1)
+    w2, i2 = O.route_topk_fp64(np.array([[0.7, -0.4]]), 1, renormalize=False)
+    assert i2[0, 0] == 0 and abs(w2[0, 0] - 1.0 / (1.0 + math.exp(-1.1))) < 1e-15
+    w3, _ = O.route_topk_fp64(np.array([[0.7, -0.4]]), 1, renormalize=True)
+    assert w3[0, 0] == 1.0
+    # ties: descending logit, then ascending expert id (brute force)
+    t = np.array([[1.0, 3.0, 3.0, 0.0, 3.0, 1.0]])
+    wt, it = O.route_topk_fp64(t, 4, renormalize=True)
+    brute = sorted(range(6), key=lambda e: (-t[0, e], e))[:4]
+    assert it[0].tolist() == brute == [1, 2, 4, 0]
+    assert wt[0, 0] == wt[0, 1] == wt[0, 2] and abs(wt.sum() - 1.0) < 1e-15
