@@ -362,14 +362,19 @@ def test_moe_layer_fp16_multi_round_grid():
     assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="fp16 layer, several rounds")
 
 
-@pytest.mark.parametrize("m,n,dtype", [(2300, 3072, torch.float16), (2048, 2048, torch.bfloat16)])
-def test_routed_gemm_multi_round_grid(m, n, dtype):
-    # 68-75 routed 128-row blocks: more tiles than resident workgroups (the
-    # persistent kernel; 128 x 256 tiles at N = 3072, whose rounds are 88%
-    # full, 128 x 128 at N = 2048).  Expert -1 blocks, ids outside [0, E)
-    # (rows left untouched), route weights, per-expert scales
-    rng = np.random.default_rng(n)
-    k, e, top_k, block_m = 256, 8, 4, 128
+@pytest.mark.parametrize("m,n,k,dtype,block_m",
+                         [(2300, 3072, 256, torch.float16, 128),
+                          (2048, 2048, 256, torch.bfloat16, 128),
+                          (1200, 2048, 256, torch.float16, 64),
+                          (1600, 1536, 768, torch.bfloat16, 64)])
+def test_routed_gemm_multi_round_grid(m, n, k, dtype, block_m):
+    # several rounds of tiles: 68-75 routed 128-row blocks (the persistent
+    # kernel; 128 x 256 tiles at N = 3072, whose rounds are 88% full,
+    # 128 x 128 at N = 2048), or 83-108 blocks of 64 rows (64 x 128 tiles,
+    # 3 stages).  Expert -1 blocks, ids outside [0, E) (rows left
+    # untouched), route weights, per-expert scales
+    rng = np.random.default_rng(n + k)
+    e, top_k = 8, 4
     wp, ws = rand_mxfp4(rng, (e, n), k)
     a = rand_act(n + 1, (m, k), dtype)
     w, ids = _route(m, e, top_k, n + 2)
