@@ -4,13 +4,14 @@
 // them (test:242-244: softmax -> torch.topk) and, with renormalisation, the
 // way the MoE benchmark configuration does (softmax -> top-k -> w / sum w).
 //
-// One wave per token row; lane l holds the logits of experts l, l + 64, ...
+// L lanes per token row (16 when E <= 256 and k <= 16: four rows per wave;
+// else 64); lane l of a row holds the logits of experts l, l + L, ...
 // Selection compares logits, not probabilities: softmax is monotonic, so the
 // top-k of the probabilities is the top-k of the logits, with no rounding in
-// between.  k rounds of a wave-wide argmax, ties to the lower expert id;
-// slot r of the result is the r-th largest.  A few rows take as long as one
-// wave's chain of k argmax reductions, hence DPP for the cross-lane steps
-// (below).  Weights:
+// between.  k rounds of an argmax over the row's lanes, ties to the lower
+// expert id; slot r of the result is the r-th largest.  A few rows take as
+// long as one chain of k argmax reductions, hence DPP for the cross-lane
+// steps (below).  Weights:
 //   p_i = exp(l_i - max) / sum_j exp(l_j - max)
 //   renormalised: p_i / sum_{s selected} p_s = exp(l_i - max) / sum_s exp(l_s - max)
 // (the full denominator cancels).  FP32 throughout; the sums run as a wave
@@ -30,6 +31,9 @@ namespace {
 // yields `old`, the operation's identity.
 constexpr int kShr1 = 0x111, kShr2 = 0x112, kShr4 = 0x114, kShr8 = 0x118;
 constexpr int kBcast15 = 0x142, kBcast31 = 0x143;
+// row_ror:n rotates within each 16-lane row: combining with rotations by
+// 1, 2, 4, 8 leaves the row's result in every lane of the row
+constexpr int kRor1 = 0x121, kRor2 = 0x122, kRor4 = 0x124, kRor8 = 0x128;
 
 template <int CTRL, int ROWS>
 __device__ __forceinline__ int dpp(int old, int v) {
@@ -40,8 +44,16 @@ __device__ __forceinline__ float dppf(float old, float v) {
   return __int_as_float(dpp<CTRL, ROWS>(__float_as_int(old), __float_as_int(v)));
 }
 
-// sum over the wave, returned to every lane
-__device__ __forceinline__ float wave_sum(float v) {
+// sum over the row of L lanes (16 or 64), returned to every lane of the row
+template <int L>
+__device__ __forceinline__ float row_sum(float v) {
+  if constexpr (L == 16) {
+    v += dppf<kRor1, 0xF>(0.f, v);
+    v += dppf<kRor2, 0xF>(0.f, v);
+    v += dppf<kRor4, 0xF>(0.f, v);
+    v += dppf<kRor8, 0xF>(0.f, v);
+    return v;
+  }
   v += dppf<kShr1, 0xF>(0.f, v);
   v += dppf<kShr2, 0xF>(0.f, v);
   v += dppf<kShr4, 0xF>(0.f, v);
@@ -67,35 +79,15 @@ __device__ __forceinline__ void argmax_step(float& best, int& bi) {
   take_better(best, bi, ov, oi);
 }
 
-template <int J, typename ID>
-__global__ __launch_bounds__(256) void route_topk(const float* __restrict__ logits, int64_t m,
-                                                  int ne, int64_t ld, int top_k, int renorm,
-                                                  float* __restrict__ w_out,
-                                                  ID* __restrict__ id_out) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= m) return;  // the whole wave: one row per wave, no barriers
-  const float* lr = logits + row * ld;
-  float v[J];
-#pragma unroll
-  for (int j = 0; j < J; ++j) v[j] = lane + 64 * j < ne ? lr[lane + 64 * j] : -INFINITY;
-
-  uint32_t taken = 0;  // bit j: expert lane + 64 j already selected
-  float mine = -INFINITY;  // slot `lane` (lanes < top_k): logit and expert
-  int mine_id = 0;
-  for (int r = 0; r < top_k; ++r) {
-    // the lane's best unselected expert (ascending j: ties keep the lower id)
-    float best = -INFINITY;
-    int bi = INT_MAX;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int e = lane + 64 * j;
-      if (e < ne && !((taken >> j) & 1u) && (bi == INT_MAX || v[j] > best)) {  // ties: lower j
-        best = v[j];
-        bi = e;
-      }
-    }
-    // wave argmax into lane 63, then to every lane
+// argmax over the row of L lanes, returned to every lane of the row
+template <int L>
+__device__ __forceinline__ void row_argmax(float& best, int& bi) {
+  if constexpr (L == 16) {
+    argmax_step<kRor1, 0xF>(best, bi);
+    argmax_step<kRor2, 0xF>(best, bi);
+    argmax_step<kRor4, 0xF>(best, bi);
+    argmax_step<kRor8, 0xF>(best, bi);
+  } else {
     argmax_step<kShr1, 0xF>(best, bi);
     argmax_step<kShr2, 0xF>(best, bi);
     argmax_step<kShr4, 0xF>(best, bi);
@@ -104,24 +96,58 @@ __global__ __launch_bounds__(256) void route_topk(const float* __restrict__ logi
     argmax_step<kBcast31, 0xC>(best, bi);
     best = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best), 63));
     bi = __builtin_amdgcn_readlane(bi, 63);
+  }
+}
+
+template <int L, int J, typename ID>
+__global__ __launch_bounds__(256) void route_topk(const float* __restrict__ logits, int64_t m,
+                                                  int ne, int64_t ld, int top_k, int renorm,
+                                                  float* __restrict__ w_out,
+                                                  ID* __restrict__ id_out) {
+  static_assert(L == 16 || L == 64, "16 or 64 lanes per row");
+  const int lane = threadIdx.x & (L - 1);  // lane within the row
+  const int64_t row = (int64_t)blockIdx.x * (256 / L) + threadIdx.x / L;
+  if (row >= m) return;  // whole rows of lanes; no barriers
+  const float* lr = logits + row * ld;
+  float v[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) v[j] = lane + L * j < ne ? lr[lane + L * j] : -INFINITY;
+
+  uint32_t taken = 0;  // bit j: expert lane + L j already selected
+  float mine = -INFINITY;  // slot `lane` (lanes < top_k): logit and expert
+  int mine_id = 0;
+  float top = 0.f;  // the row's largest logit (round 0)
+  for (int r = 0; r < top_k; ++r) {
+    // the lane's best unselected expert (ascending j: ties keep the lower id)
+    float best = -INFINITY;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int e = lane + L * j;
+      if (e < ne && !((taken >> j) & 1u) && (bi == INT_MAX || v[j] > best)) {  // ties: lower j
+        best = v[j];
+        bi = e;
+      }
+    }
+    row_argmax<L>(best, bi);
+    if (r == 0) top = best;
     if (lane == r) {
       mine = best;
       mine_id = bi;
     }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    if ((bi & (L - 1)) == lane) taken |= 1u << (bi / L);
   }
 
-  const float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), 0));
   const float ex = lane < top_k ? expf(mine - top) : 0.f;
   float denom;
   if (renorm) {
-    denom = wave_sum(ex);
+    denom = row_sum<L>(ex);
   } else {
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < J; ++j)
-      if (lane + 64 * j < ne) s += expf(v[j] - top);
-    denom = wave_sum(s);
+      if (lane + L * j < ne) s += expf(v[j] - top);
+    denom = row_sum<L>(s);
   }
   if (lane < top_k) {
     w_out[row * top_k + lane] = ex / denom;
@@ -129,16 +155,26 @@ __global__ __launch_bounds__(256) void route_topk(const float* __restrict__ logi
   }
 }
 
+template <int L, typename ID>
+void launch_rows(const float* logits, int64_t m, int ne, int64_t ld, int top_k, int renorm,
+                 float* w, ID* ids, hipStream_t st) {
+  constexpr int R = 256 / L;  // rows per workgroup
+  const unsigned grid = (unsigned)((m + R - 1) / R);
+  const int j = (ne + L - 1) / L;
+  if (j <= 1) route_topk<L, 1, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
+  else if (j <= 2) route_topk<L, 2, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
+  else if (j <= 4) route_topk<L, 4, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
+  else if (j <= 8) route_topk<L, 8, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
+  else route_topk<L, 16, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
+}
+
 template <typename ID>
 int launch_route(const float* logits, int64_t m, int ne, int64_t ld, int top_k, int renorm,
                  float* w, ID* ids, hipStream_t st) {
-  const unsigned grid = (unsigned)((m + 3) / 4);
-  const int j = (ne + 63) / 64;
-  if (j <= 1) route_topk<1, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
-  else if (j <= 2) route_topk<2, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
-  else if (j <= 4) route_topk<4, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
-  else if (j <= 8) route_topk<8, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
-  else route_topk<16, ID><<<grid, 256, 0, st>>>(logits, m, ne, ld, top_k, renorm, w, ids);
+  // 16 lanes per row (4 rows per wave) while a row's logits fit 16 per
+  // lane and its slots one per lane
+  if (ne <= 256 && top_k <= 16) launch_rows<16>(logits, m, ne, ld, top_k, renorm, w, ids, st);
+  else launch_rows<64>(logits, m, ne, ld, top_k, renorm, w, ids, st);
   return launch_status("router launch");
 }
 
