@@ -142,6 +142,8 @@ enum PfConfig {
   PF_128x320 = 4,  // 1 x 4 waves of 128 x 80 (plain store epilogue only)
 };
 bool pf_supported(const GemmArgs& g, int elem_bytes);
+// Compute units of the current device (cached per device; 0 if unknown).
+int device_cus();
 int pf_choose(const GemmArgs& g, int epi);
 int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t st);
 // Split-K plan for a dense plain-epilogue GEMM whose tiles would not fill

@@ -730,19 +730,6 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
   }
 }
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB>
 int launch_cfg(const GemmArgs& g, hipStream_t st) {
   typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
@@ -824,6 +811,19 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
 }
 
 }  // namespace
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
 
 bool pf_supported(const GemmArgs& g, int elem_bytes) {
   if (g.k % 128 != 0 || g.k <= 0 || g.a_rows <= 0) return false;

@@ -227,6 +227,11 @@ int launch_typed(const DownArgs& a, hipStream_t st) {
     return MXFP4_ERR_VALUE;
   }
   dim3 grid((unsigned)(a.hidden / a.cw), (unsigned)gy);
+  // When the grid holds more waves than are resident at once (16 per CU
+  // at this kernel's ~114 VGPRs), two K waves with up to two trips each
+  // beat three or four with one (MoE layer M=8: 42.9 -> 40.0 us; M=1,
+  // resident either way, stays on four: 15.1 vs 16.3 us with two)
+  if (wk > 2 && (int64_t)grid.x * grid.y * rw * wk > (int64_t)device_cus() * 16) wk = 2;
   switch (rw) {
     case 1: return launch_rw<T, 1>(a, wk, u, grid, st);
     case 2: return launch_rw<T, 2>(a, wk, u, grid, st);
