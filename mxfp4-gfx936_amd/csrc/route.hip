@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void route_topk(const float* __restrict__ logi
   uint32_t taken = 0;  // bit j: expert lane + L j already selected
   float mine = -INFINITY;  // slot `lane` (lanes < top_k): logit and expert
   int mine_id = 0;
-  float top = 0.f;  // the row's largest logit (round 0)
+  float top = 0.f;  // the row's largest logit (first argmax pass)
   for (int r = 0; r < top_k; ++r) {
     // the lane's best unselected expert (ascending j: ties keep the lower id)
     float best = -INFINITY;
