@@ -23,7 +23,11 @@ MALL cannot serve them, launches replayed from a HIP graph), the routed MoE
 layer (us), W4A4 on the block-scaled FP4 MFMA, and the standalone dequant.
 ``cpu_baseline`` times the reference safe path (explicit dequant +
 torch.matmul bf16, restated in oracle/) on this host's cores on a bounded
-row sample of the headline workload.
+row sample of the headline workload; ``cpu_config1`` times it on BASELINE
+config 1 (M=64, K=2048, N=2048; seconds and GFLOP/s), and every sweep row
+carries ``cpu_ms``, the same restatement at that row's shape (the MoE layer
+as the per-expert loop of the safe op composed as the vLLM layer), under a
+per-row time cap.
 """
 
 from __future__ import annotations
@@ -364,10 +368,7 @@ def cpu_baseline(np, m, k, n, budget_s=20.0):
     dequant -> torch.matmul bf16), timed on this host on a row sample."""
     import torch
     from oracle import mxfp4_oracle as O
-    threads = len(os.sched_getaffinity(0))
-    if os.environ.get("OMP_NUM_THREADS", "").isdigit():  # the host share given to this job
-        threads = max(1, min(threads, int(os.environ["OMP_NUM_THREADS"])))
-    torch.set_num_threads(threads)
+    threads, isa = _cpu_setup()
     rng = np.random.default_rng(20260812)
     w = torch.from_numpy(rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8))
     s = torch.from_numpy(rng.integers(120, 129, size=(n, k // 32), dtype=np.uint8))
@@ -389,6 +390,20 @@ def cpu_baseline(np, m, k, n, budget_s=20.0):
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
     flops = 2.0 * rows * n * k
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"safe path (dequant + torch.matmul bf16) on x[{rows},{k}] x W[{n},{k}], "
+                      f"median of {len(times)} calls ({t * 1e3:.1f} ms each), torch "
+                      f"{torch.__version__}, isa {isa}"}
+
+
+def _cpu_setup():
+    """Threads for the CPU legs (the host share given to this job) and the ISA."""
+    import torch
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = max(1, min(threads, int(os.environ["OMP_NUM_THREADS"])))
+    torch.set_num_threads(threads)
     isa = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -396,11 +411,95 @@ def cpu_baseline(np, m, k, n, budget_s=20.0):
         isa = ",".join(x for x in ("avx512_bf16", "amx_bf16", "avx512f", "avx2") if x in flags.split())
     except OSError:
         pass
-    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"safe path (dequant + torch.matmul bf16) on x[{rows},{k}] x W[{n},{k}], "
-                      f"median of {len(times)} calls ({t * 1e3:.1f} ms each), torch "
-                      f"{torch.__version__}, isa {isa}"}
+    return threads, isa
+
+
+def _time_cpu(fn, cap_s, max_runs=5):
+    """One warm-up call, then up to max_runs timed calls while the timed total
+    stays under cap_s (at least one); returns (median seconds, runs)."""
+    import numpy as np
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_runs and (not times or time.perf_counter() - t_start < cap_s):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_config1(np):
+    """the reference safe path (oracle/mxfp4_oracle.py
+    linear_safe: explicit dequant -> torch.matmul bf16) on the host, x bf16
+    [64, 2048] ~ N(0, 1), W u8 [2048, 1024] codes uniform 0..15, S u8
+    [2048, 64] uniform 120..128; seconds and GFLOP/s per call."""
+    import torch
+    from oracle import mxfp4_oracle as O
+    threads, isa = _cpu_setup()
+    m, k, n = 64, 2048, 2048
+    rng = np.random.default_rng(20260810)
+    w = torch.from_numpy(rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8))
+    s = torch.from_numpy(rng.integers(120, 129, size=(n, k // 32), dtype=np.uint8))
+    x = torch.randn((m, k), generator=torch.Generator().manual_seed(20260810)).to(torch.bfloat16)
+    t, runs = _time_cpu(lambda: O.linear_safe(x, w, s), cap_s=10.0, max_runs=9)
+    flops = 2.0 * m * n * k
+    return {"seconds": round(t, 6), "GFLOP/s": round(flops / t / 1e9, 2), "flops": int(flops),
+            "runs": runs, "cores": threads, "isa": isa, "torch": torch.__version__,
+            "kind": "port", "what": "safe path restated: dequant_safe + torch.matmul bf16"}
+
+
+CPU_CAP_S = {"linear": 3.0, "moe": 12.0, "w4a4": 6.0}
+
+
+def cpu_beside_sweep(np, res):
+    """The same CPU restatement of the safe path at each sweep row's shape,
+    added to that row as cpu_ms (median of up to 5 calls after one warm-up,
+    within CPU_CAP_S seconds per row; cpu_runs says how many were timed)."""
+    import torch
+    from oracle import mxfp4_oracle as O
+    _cpu_setup()
+    g = torch.Generator().manual_seed(20260813)
+    rng = np.random.default_rng(20260813)
+
+    def weights(rows, k):
+        return (torch.from_numpy(rng.integers(0, 256, size=(*rows, k // 2), dtype=np.uint8)),
+                torch.from_numpy(rng.integers(120, 129, size=(*rows, k // 32), dtype=np.uint8)))
+
+    def put(key, fn, cap):
+        if key not in res:
+            return
+        t, runs = _time_cpu(fn, cap)
+        res[key]["cpu_ms"] = round(t * 1e3, 3)
+        res[key]["cpu_runs"] = runs
+        res[key]["gpu_speedup"] = round(t * 1e3 / res[key]["us"] * 1e3, 1)
+        log(f"cpu {key}: {t * 1e3:.1f} ms ({runs} runs)")
+
+    for name, k, n in (("qkv", 2048, 5120), ("o_proj", 4096, 2048)):
+        w, s = weights((n,), k)
+        for m in (1, 8, 370, 4096):
+            x = torch.randn((m, k), generator=g).to(torch.bfloat16)
+            put(f"w4a16_{name}_m{m}", lambda x=x, w=w, s=s: O.linear_safe(x, w, s),
+                CPU_CAP_S["linear"])
+    e, hidden, inter, top_k = 128, 2048, 768, 8
+    w13, s13 = weights((e, 2 * inter), hidden)
+    w2, s2 = weights((e, hidden), inter)
+    for m in (1, 8, 32, 512, 4096):
+        logits = torch.randn((m, e), generator=g)
+        tw, ids = torch.topk(torch.softmax(logits, -1), top_k, dim=-1)
+        tw = tw / tw.sum(-1, keepdim=True)
+        x = torch.randn((m, hidden), generator=g).to(torch.bfloat16)
+        put(f"moe_layer_m{m}",
+            lambda x=x, tw=tw, ids=ids: O.moe_layer_safe(x, w13, s13, w2, s2, tw, ids),
+            CPU_CAP_S["moe"])
+    # W4A4 = the soft op with one expert and packed A (soft:468-494)
+    m, k, n = 8192, 4096, 4096
+    ap, asc = weights((m,), k)
+    bp, bsc = weights((1, n), k)
+    c = torch.empty((m, 1, n), dtype=torch.bfloat16)
+    ones, ids1 = torch.ones(1), torch.zeros((m, 1), dtype=torch.int64)
+    put("w4a4_8192x4096x4096",
+        lambda: O.fused_moe_safe(ap, bp, c, ones, ones, asc, bsc, ones.expand(m, 1), ids1, False),
+        CPU_CAP_S["w4a4"])
 
 
 def main() -> int:
@@ -489,6 +588,11 @@ def main() -> int:
     if not args.no_cpu:
         log("cpu baseline (bounded sample)")
         out["cpu_baseline"] = cpu_baseline(np, m, k, n)
+        log("cpu: BASELINE config 1")
+        out["cpu_config1"] = cpu_config1(np)
+        if "sweep" in out:
+            log("cpu: the safe path beside each sweep row")
+            cpu_beside_sweep(np, out["sweep"])
     print(json.dumps(out), flush=True)
     return 0
 

@@ -540,6 +540,10 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_stream(GemmArgs g) {
   static_for<0, CS>([&](auto step_c) {
     constexpr int s = decltype(step_c)::value;
     constexpr int b = s & 1;
+    // the wait below lets the next step's loads stay in flight and counts
+    // on every earlier load (the staging copies above all) having been
+    // issued before them: a compiler fence keeps that order
+    if constexpr (s == 0) asm volatile("" ::: "memory");
     if constexpr (s + 1 < CS) load_step(s + 1, std::integral_constant<int, b ^ 1>{});
     if constexpr (s == 0) {
       // the staged rows have landed once at most the next step's loads

@@ -29,6 +29,8 @@
 // Requirements (else the host falls back to the register-staged kernel):
 // K % 128 == 0; activation and weight byte ranges below 2 GiB; 16-byte
 // aligned A / B rows and 4-byte aligned scale rows.
+#include <atomic>
+
 #include "gemm.h"
 
 namespace mx {
@@ -274,8 +276,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
+  // the stage waits count loads per stage in issue order: a compiler fence
+  // after each prologue stage keeps stage s + 1's loads behind stage s's
+  for (int s = 0; s < STAGES - 1; ++s) {
     if (k_begin + s < k_end) issue(k_begin + s);
+    asm volatile("" ::: "memory");
+  }
   for (int kt = k_begin; kt < k_end; ++kt) {
     // Stage kt has landed once at most the later stages' loads are
     // outstanding.  A bare s_barrier (not __syncthreads, whose release fence
@@ -750,11 +756,15 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
     const int64_t c_bytes = g.num_valid * g.ldc * (int64_t)sizeof(T);
     if (g.sorted_ids && g.n % 4 == 0 && g.ldc % 4 == 0 && c_bytes < (int64_t)0x7FFFFFFF) {
       auto kern = w4a16_pp<T, FM, FN, EPI, MINB>;
-      static int per_cu = -1;  // same on every device of the build target
+      // same on every device of the build target; threads that race here
+      // store the same value
+      static std::atomic<int> per_cu_cache{-1};
+      int per_cu = per_cu_cache.load(std::memory_order_relaxed);
       if (per_cu < 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, S::NT, 0) != hipSuccess) nb = 0;
         per_cu = nb;
+        per_cu_cache.store(nb, std::memory_order_relaxed);
       }
       const int64_t slots = ((int64_t)per_cu * device_cus()) & ~(int64_t)7;
       if (slots >= 8 && nwg > slots) {
@@ -814,15 +824,16 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
 
 // Compute units of the current device (cached per device).
 int device_cus() {
-  static int cus[64] = {0};
+  // per device; threads that race here store the same value
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 bool pf_supported(const GemmArgs& g, int elem_bytes) {

@@ -196,8 +196,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
   const int sb_rd = (wn * FN * 16 + c16) * 4 + grp;
 
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
+  // the stage waits count loads per stage in issue order: a compiler fence
+  // after each prologue stage keeps stage s + 1's loads behind stage s's
+  for (int s = 0; s < STAGES - 1; ++s) {
     if (s < nk) issue(s);
+    asm volatile("" ::: "memory");
+  }
   for (int kt = 0; kt < nk; ++kt) {
     // stage kt has landed once at most the later stages' loads of this wave
     // are outstanding (PER_STAGE each); the barrier publishes it and retires

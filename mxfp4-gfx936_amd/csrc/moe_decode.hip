@@ -24,6 +24,11 @@ namespace mx {
 namespace {
 
 constexpr int kRG = 4;  // routes per wave
+// Compute units the launch choices below assume (MI355X).  The K-wave count
+// decides how K partial sums are grouped, so deriving it from the device
+// would make the output bits depend on the SKU or partition mode; with a
+// fixed model they depend on the inputs and shapes only.
+constexpr int kModelCUs = 256;
 
 struct DownArgs {
   const void* h;          // [routes, inter] of T
@@ -231,7 +236,7 @@ int launch_typed(const DownArgs& a, hipStream_t st) {
   // at this kernel's ~114 VGPRs), two K waves with up to two trips each
   // beat three or four with one (MoE layer M=8: 42.9 -> 40.0 us; M=1,
   // resident either way, stays on four: 15.1 vs 16.3 us with two)
-  if (wk > 2 && (int64_t)grid.x * grid.y * rw * wk > (int64_t)device_cus() * 16) wk = 2;
+  if (wk > 2 && (int64_t)grid.x * grid.y * rw * wk > (int64_t)kModelCUs * 16) wk = 2;
   switch (rw) {
     case 1: return launch_rw<T, 1>(a, wk, u, grid, st);
     case 2: return launch_rw<T, 2>(a, wk, u, grid, st);
@@ -269,7 +274,7 @@ int launch_moe_down_topk(const void* h, const uint8_t* w2, const uint8_t* s2,
   a.tpt = 1;
   // 8 columns per workgroup when 16 would give fewer workgroups than CUs
   // (M=1: 128 -> 256 workgroups; MoE layer at M=1: 15.4 -> 15.1 us)
-  a.cw = (hidden / 16) * m < 256 ? 8 : 16;
+  a.cw = (hidden / 16) * m < kModelCUs ? 8 : 16;
   if (m == 0) return MXFP4_OK;
   return dtype == MXFP4_DT_BF16 ? launch_typed<__bf16>(a, st) : launch_typed<_Float16>(a, st);
 }

@@ -90,9 +90,9 @@ def fused_moe_mxfp4(
     if num_tokens_post_padded.numel() != 1:
         raise RuntimeError("num_tokens_post_padded must hold one value")
 
-    device = _lib.require_device(A, B, C, sorted_token_ids, expert_ids, num_tokens_post_padded)
     act, act_mx, b, b_mx, a_scale, b_scale, weights, ids = _prepare_moe_operands(
         A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights, topk_ids, top_k)
+    device = _lib.require_device(A, B, C, sorted_token_ids, expert_ids, num_tokens_post_padded)
     num_routes = ids.numel()
     if em == 0 or C.numel() == 0:
         return

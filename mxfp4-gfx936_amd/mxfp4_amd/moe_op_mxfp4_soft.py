@@ -16,6 +16,7 @@ path with importlib, as the reference tests load their module (test:10-19).
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import sys
 
@@ -36,6 +37,15 @@ _MXFP4_E2M1_VALUES = (
 _KERNEL_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
+@functools.lru_cache(maxsize=1)
+def _has_compatible_triton_compiler() -> bool:
+    """soft:34-42 (policy name kept).  The reference probes for the DTK clang
+    its Triton kernels need; this backend's kernels are compiled ahead of
+    time, so what ``MXFP4_GFX936_BACKEND=triton`` needs is the built HIP
+    library.  True when that file exists."""
+    return os.path.isfile(_lib.LIB_PATH)
+
+
 def _backend() -> str:
     """soft:45-49: ``MXFP4_GFX936_BACKEND`` in {safe, triton}, default safe;
     anything else fails loudly.  Both values select the HIP kernels here."""
@@ -43,6 +53,24 @@ def _backend() -> str:
     if backend not in ("safe", "triton"):
         raise ValueError(f"unknown gfx936 MXFP4 backend: {backend}")
     return backend
+
+
+def _require_triton_compiler() -> None:
+    """soft:52-57: the ``triton`` backend value fails loudly, with the
+    reference's message, when ``_has_compatible_triton_compiler`` says no
+    (looked up at call time, so a monkeypatched probe is honoured)."""
+    if not _has_compatible_triton_compiler():
+        raise RuntimeError(
+            "MXFP4_GFX936_BACKEND=triton requires a compatible compiler; "
+            "set TRITON_HIP_CLANG_PATH explicitly"
+        )
+
+
+def _is_validated_triton_linear_shape(m: int, n: int) -> bool:
+    """soft:60-62: the reference's fused-kernel shape guard (M >= 370 and
+    N >= 2048).  Kept as policy: every shape runs the HIP kernels here, and
+    the kernel is chosen from the shape by the library itself."""
+    return m >= 370 and n >= 2048
 
 
 def _routing_block_m(num_routes: int, num_experts: int) -> int:
@@ -144,7 +172,8 @@ def linear_mxfp4_soft(
         raise ValueError("one E8M0 scale is required for every 32 MXFP4 values")
 
     input_shape = x.shape
-    _backend()
+    if _backend() == "triton":
+        _require_triton_compiler()  # soft:333-334
     device = _lib.require_device(x, packed, block_scales, bias)
     lib = _lib.load()
     n = packed.shape[0]
@@ -228,11 +257,21 @@ def _prepare_moe_operands(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, top
     if A.dtype == torch.uint8:
         if A_mx_scale is None:
             raise ValueError("packed MXFP4 activations require A_mx_scale")
-        if A.ndim != 2 or A.shape[1] * 2 != logical_k or A_mx_scale.shape != (
-                A.shape[0], logical_k // 32):
-            raise RuntimeError("packed activations must be [M, K/2] with A_mx_scale [M, K/32]")
+        # the reference dequantizes packed A with dequant_mxfp4 (soft:471),
+        # whose checks (soft:283-294) give these exception types
         if A_mx_scale.dtype != torch.uint8:
-            raise TypeError("A_mx_scale must be uint8")
+            raise TypeError(f"block_scales must be uint8, got {A_mx_scale.dtype}")
+        a_k = A.shape[-1] * 2
+        if a_k % 32 != 0:
+            raise ValueError(f"logical K must be divisible by 32, got {a_k}")
+        if A_mx_scale.shape[:-1] != A.shape[:-1]:
+            raise ValueError("packed and block_scales leading dimensions must match")
+        if A_mx_scale.shape[-1] * 32 != a_k:
+            raise ValueError("one E8M0 scale is required for every 32 MXFP4 values")
+        # a K or rank the expert GEMM cannot take fails in the reference's
+        # matmul (soft:487-490), a RuntimeError
+        if A.ndim != 2 or a_k != logical_k:
+            raise RuntimeError("packed activations must be [M, K/2] with A_mx_scale [M, K/32]")
         act = _lib.aligned(A)
         act_mx = A_mx_scale.contiguous()
     else:
@@ -249,6 +288,9 @@ def _prepare_moe_operands(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, top
             f"C must be [M, top_k, N] = {(m, top_k, B.shape[1])}, got {tuple(C.shape)}")
     if act.shape[0] < m:
         raise RuntimeError("fewer activation rows than top-k rows")
+    if A_scale.numel() == 0:
+        # the reference reads A_scale.reshape(-1)[0] (soft:477)
+        raise IndexError("index 0 is out of bounds for dimension 0 with size 0")
     a_scale = A_scale.reshape(-1)[:1].to(torch.float32).contiguous()
     if B_scale.numel() < B.shape[0]:
         raise RuntimeError("B_scale must hold one scale per expert")
@@ -287,7 +329,10 @@ def fused_moe_mxfp4_soft(
     or packed MXFP4 with ``A_mx_scale`` (W4A4 on the block-scaled MFMA).
     Like the reference's safe path, the routing metadata arguments are not
     consulted (soft:466): routing is rebuilt on the device from ``topk_ids``
-    with no host synchronisation.
+    with no host synchronisation.  With ``MXFP4_GFX936_BACKEND=triton`` the
+    reference's checks of that backend run first (soft:410-427: compiler,
+    unpacked activations, non-empty metadata of a supported block size, K a
+    multiple of 128; RuntimeError otherwise); the result is the same one.
     """
     if swizzle_mx_a or swizzle_mx_b:
         raise NotImplementedError("the gfx936 software fallback does not support swizzled scales")
@@ -300,12 +345,30 @@ def fused_moe_mxfp4_soft(
     if matmul_dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise TypeError(f"unsupported software fallback compute dtype: {matmul_dtype}")
 
-    _backend()
+    if _backend() == "triton":
+        _require_triton_compiler()
+        routing_ready = (
+            A.dtype != torch.uint8
+            and sorted_token_ids.numel() > 0
+            and expert_ids.numel() > 0
+            and num_tokens_post_padded.numel() == 1
+            and B.shape[-1] * 2 % 128 == 0
+            and sorted_token_ids.numel() % expert_ids.numel() == 0
+        )
+        if not routing_ready:
+            raise RuntimeError(
+                "the experimental Triton MoE backend requires unpacked "
+                "activations and valid padded routing metadata"
+            )
+        block_m = sorted_token_ids.numel() // expert_ids.numel()
+        if block_m not in (16, 32, 64, 128):
+            raise RuntimeError(f"unsupported Triton routing block size: {block_m}")
     del sorted_token_ids, expert_ids, num_tokens_post_padded
-    device = _lib.require_device(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale,
-                                 topk_weights, topk_ids)
+    # operand checks first (soft:468-477), then the device
     act, act_mx, b, b_mx, a_scale, b_scale, weights, ids = _prepare_moe_operands(
         A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights, topk_ids, top_k)
+    device = _lib.require_device(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale,
+                                 topk_weights, topk_ids)
 
     C.zero_()
     num_routes = ids.numel()

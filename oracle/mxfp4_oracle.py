@@ -110,6 +110,22 @@ def round_to_dtype(values: np.ndarray, dtype: str) -> np.ndarray:
 # Dequant (soft:277-307)
 # ----------------------------------------------------------------------------
 
+_FMT_BITS = {"bf16": (7, -133), "f16": (10, -24), "f32": (23, -149)}
+
+
+def format_ulp(values: np.ndarray, dtype: str) -> np.ndarray:
+    """Spacing of the ``dtype`` grid (bf16 / f16 / f32) at |values|: 2^(e - p)
+    for |v| in [2^e, 2^(e+1)) with p explicit mantissa bits, never below
+    the format's smallest subnormal.  0 at non-finite values."""
+    mant, sub = _FMT_BITS[dtype]
+    v = np.abs(np.asarray(values, dtype=np.float64))
+    fin = np.isfinite(v)
+    _, ex = np.frexp(np.where(fin & (v > 0), v, 1.0))
+    ulp = np.where(v > 0, np.ldexp(1.0, ex - 1 - mant), 0.0)
+    ulp = np.maximum(ulp, np.ldexp(1.0, sub))
+    return np.where(fin, ulp, 0.0)
+
+
 def unpack_codes(packed: np.ndarray) -> np.ndarray:
     """Packed bytes [..., K/2] -> codes [..., K]; the low nibble is the even k
     (soft:295)."""
@@ -343,12 +359,15 @@ def linear_fp64(x: np.ndarray, packed: np.ndarray, scales: np.ndarray,
 def fused_moe_fp64(a_values: np.ndarray, b_packed: np.ndarray, b_mx: np.ndarray,
                    a_scale: float, b_scale: np.ndarray, topk_weights: np.ndarray,
                    topk_ids: np.ndarray, mul_routed_weight: bool,
-                   compute_dtype: str = "bf16") -> np.ndarray:
+                   compute_dtype: str = "bf16", b_values=None) -> np.ndarray:
     """C[t, s, :] = a[t] . dequant(B[e])^T * a_scale * b_scale[e] (* w[t, s])
     for e = topk_ids[t, s] in [0, E); other slots are 0 (soft:476-494).
 
     ``a_values`` are the activations already at the compute dtype (the caller
-    dequantizes packed A, soft:468-475).  Accumulates in float64."""
+    dequantizes packed A, soft:468-475).  Accumulates in float64.
+    ``b_values`` (optional): a callable e -> ``dequant_values(b_packed[e],
+    b_mx[e], compute_dtype)`` computed once by the caller, for tests that
+    evaluate many cases over the same experts."""
     a = np.asarray(a_values, dtype=np.float64)
     ids = np.asarray(topk_ids).astype(np.int64)
     m, top_k = ids.shape
@@ -358,7 +377,10 @@ def fused_moe_fp64(a_values: np.ndarray, b_packed: np.ndarray, b_mx: np.ndarray,
         t, s = np.nonzero(ids == e)
         if t.size == 0:
             continue
-        w = dequant_values(b_packed[e], b_mx[e], compute_dtype)
+        if b_values is not None:
+            w = np.asarray(b_values(e), dtype=np.float64)
+        else:
+            w = dequant_values(b_packed[e], b_mx[e], compute_dtype)
         v = (a[t] @ w.T) * float(a_scale) * float(b_scale[e])
         if mul_routed_weight:
             v = v * np.asarray(topk_weights, dtype=np.float64)[t, s, None]
@@ -378,20 +400,27 @@ def silu_mul_bf16(gate_up_bf16: np.ndarray) -> np.ndarray:
 
 
 def moe_layer_fp64(x: np.ndarray, w13: np.ndarray, s13: np.ndarray, w2: np.ndarray,
-                   s2: np.ndarray, topk_weights: np.ndarray, topk_ids: np.ndarray) -> np.ndarray:
+                   s2: np.ndarray, topk_weights: np.ndarray, topk_ids: np.ndarray,
+                   w13_values=None, w2_values=None, return_routes: bool = False):
     """The vLLM MoE layer (vllm:233-265) with float64 GEMMs and the
     reference's rounding points: gate_up rounded to bf16 per route, silu*mul
     in bf16, the route-weighted down output rounded to bf16 per route, then
-    the top-k sum (accumulated in float64 here).  Returns float64 [M, H]."""
+    the top-k sum (accumulated in float64 here).  Returns float64 [M, H].
+    ``w13_values`` / ``w2_values``: optional pre-dequantized experts, as
+    ``b_values`` of fused_moe_fp64.  With ``return_routes`` also returns the
+    per-route down outputs after their bf16 rounding, [M, top_k, H] (the
+    values the reference rounds before the top-k sum, vllm:253-265)."""
     m, top_k = np.asarray(topk_ids).shape
     ones_e = np.ones(w13.shape[0])
-    gu = fused_moe_fp64(x, w13, s13, 1.0, ones_e, topk_weights, topk_ids, False)
+    gu = fused_moe_fp64(x, w13, s13, 1.0, ones_e, topk_weights, topk_ids, False,
+                        b_values=w13_values)
     gu = round_to_dtype(gu, "bf16")
     h = silu_mul_bf16(gu).reshape(m * top_k, -1)
     down = fused_moe_fp64(h, w2, s2, 1.0, ones_e, np.asarray(topk_weights).reshape(-1, 1),
-                          np.asarray(topk_ids).reshape(-1, 1), True)
-    down = round_to_dtype(down, "bf16")
-    return down[:, 0].reshape(m, top_k, -1).sum(axis=1)
+                          np.asarray(topk_ids).reshape(-1, 1), True, b_values=w2_values)
+    down = round_to_dtype(down, "bf16")[:, 0].reshape(m, top_k, -1)
+    y = down.sum(axis=1)
+    return (y, down) if return_routes else y
 
 
 # ----------------------------------------------------------------------------

@@ -257,3 +257,72 @@ def test_route_topk_argument_errors():
     assert lib.mxfp4_moe_route(None, 4, 8, 8, 9, 1, None, None, i64, None) == _lib.ERR_VALUE
     assert lib.mxfp4_moe_route(None, 4, 2048, 2048, 2, 1, None, None, i64, None) == _lib.ERR_VALUE
     assert lib.mxfp4_moe_route(None, 0, 8, 8, 2, 1, None, None, i64, None) == _lib.OK
+
+
+def test_reference_policy_names(monkeypatch):
+    # soft:34-62, with the behaviour the reference tests check (test:63-78,
+    # 136-141): the shape guard, and the triton value failing loudly when the
+    # compiler probe says no (the probe is looked up at call time)
+    from mxfp4_amd import moe_op_mxfp4_soft as soft
+    assert soft._is_validated_triton_linear_shape(369, 2048) is False
+    assert soft._is_validated_triton_linear_shape(370, 2047) is False
+    assert soft._is_validated_triton_linear_shape(370, 2048) is True
+    assert soft._has_compatible_triton_compiler() is True  # the HIP library is built
+    soft._require_triton_compiler()
+    monkeypatch.setenv("MXFP4_GFX936_BACKEND", "triton")
+    monkeypatch.setattr(soft, "_has_compatible_triton_compiler", lambda: False)
+    with pytest.raises(RuntimeError, match="TRITON_HIP_CLANG_PATH"):
+        soft._require_triton_compiler()
+    x = torch.zeros((2, 128), dtype=torch.bfloat16)
+    w = torch.zeros((8, 64), dtype=torch.uint8)
+    s = torch.zeros((8, 4), dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="TRITON_HIP_CLANG_PATH"):
+        soft.linear_mxfp4_soft(x, w, s)
+    with pytest.raises(RuntimeError, match="TRITON_HIP_CLANG_PATH"):
+        soft.fused_moe_mxfp4_soft(**_moe_args())
+
+
+def test_fused_moe_triton_value_checks_metadata(monkeypatch):
+    # soft:410-427: the triton value needs unpacked activations and padded
+    # metadata of block size 16/32/64/128 (RuntimeError otherwise); the safe
+    # value ignores the metadata
+    monkeypatch.setenv("MXFP4_GFX936_BACKEND", "triton")
+    with pytest.raises(RuntimeError, match="valid padded routing metadata"):
+        mx.fused_moe_mxfp4_soft(**_moe_args())
+    meta = dict(sorted_token_ids=torch.zeros(48, dtype=torch.int32),
+                expert_ids=torch.zeros(2, dtype=torch.int32),
+                num_tokens_post_padded=torch.tensor([48], dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="block size: 24"):
+        mx.fused_moe_mxfp4_soft(**_moe_args(**meta))
+    meta["expert_ids"] = torch.zeros(3, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):  # valid: reaches the device
+        mx.fused_moe_mxfp4_soft(**_moe_args(**meta))
+    packed = _moe_args(A=torch.zeros((4, 64), dtype=torch.uint8),
+                       A_mx_scale=torch.zeros((4, 4), dtype=torch.uint8), **meta)
+    with pytest.raises(RuntimeError, match="unpacked activations"):
+        mx.fused_moe_mxfp4_soft(**packed)
+    monkeypatch.setenv("MXFP4_GFX936_BACKEND", "safe")
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        mx.fused_moe_mxfp4_soft(**packed)
+
+
+def test_fused_moe_operand_exceptions_follow_the_reference():
+    # packed A goes through the reference's dequant_mxfp4 checks (soft:471,
+    # 283-294); a K the expert GEMM cannot take fails in its matmul
+    # (RuntimeError); an empty A_scale fails its [0] read (soft:477)
+    a = torch.zeros((4, 64), dtype=torch.uint8)
+    with pytest.raises(ValueError, match="require A_mx_scale"):
+        mx.fused_moe_mxfp4_soft(**_moe_args(A=a))
+    with pytest.raises(TypeError, match="block_scales must be uint8"):
+        mx.fused_moe_mxfp4_soft(**_moe_args(A=a, A_mx_scale=torch.zeros((4, 4))))
+    with pytest.raises(ValueError, match="leading dimensions"):
+        mx.fused_moe_mxfp4_soft(**_moe_args(A=a, A_mx_scale=torch.zeros((3, 4), dtype=torch.uint8)))
+    with pytest.raises(ValueError, match="every 32"):
+        mx.fused_moe_mxfp4_soft(**_moe_args(A=a, A_mx_scale=torch.zeros((4, 2), dtype=torch.uint8)))
+    with pytest.raises(RuntimeError, match=r"\[M, K/2\]"):
+        mx.fused_moe_mxfp4_soft(**_moe_args(A=a[:, :32],
+                                            A_mx_scale=torch.zeros((4, 2), dtype=torch.uint8)))
+    with pytest.raises(ValueError, match="must not provide A_mx_scale"):
+        mx.fused_moe_mxfp4_soft(**_moe_args(A_mx_scale=torch.zeros((4, 4), dtype=torch.uint8)))
+    with pytest.raises(IndexError):
+        mx.fused_moe_mxfp4_soft(**_moe_args(A_scale=torch.ones(0)))

@@ -249,11 +249,11 @@ def test_moe_layer_vs_oracle(m, layer_weights):
     assert y.shape == (m, 2048) and y.dtype == torch.bfloat16
     # each token depends only on its own row and routing: check a sample
     rows = np.arange(m) if m <= 32 else np.sort(np.random.default_rng(m).choice(m, 32, False))
-    oracle = O.moe_layer_fp64(x.float().numpy()[rows], w13, s13, w2, s2, w.numpy()[rows],
-                              ids.numpy()[rows])
+    oracle, routes = O.moe_layer_fp64(x.float().numpy()[rows], w13, s13, w2, s2,
+                                      w.numpy()[rows], ids.numpy()[rows], return_routes=True)
     t = torch.from_numpy
     safe = O.moe_layer_safe(x[rows], t(w13), t(s13), t(w2), t(s2), w[rows], ids[rows])
-    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what=f"moe layer m={m}")
+    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what=f"moe layer m={m}", routes=routes)
 
 
 def test_vllm_adapter_moe_and_dense_on_device(layer_weights):
@@ -288,11 +288,12 @@ def test_moe_layer_hidden_not_multiple_of_128():
     w, ids = _route(m, e, top_k, 1057)
     y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
     rows = np.sort(np.random.default_rng(3).choice(m, 24, False))
-    oracle = O.moe_layer_fp64(x.float().numpy()[rows], w13, s13, w2, s2, w.numpy()[rows],
-                              ids.numpy()[rows])
+    oracle, routes = O.moe_layer_fp64(x.float().numpy()[rows], w13, s13, w2, s2,
+                                      w.numpy()[rows], ids.numpy()[rows], return_routes=True)
     t = torch.from_numpy
     safe = O.moe_layer_safe(x[rows], t(w13), t(s13), t(w2), t(s2), w[rows], ids[rows])
-    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="moe layer hidden 1056")
+    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="moe layer hidden 1056",
+                        routes=routes)
 
 
 def test_moe_layer_small_vs_golden_and_safe():
@@ -305,12 +306,17 @@ def test_moe_layer_small_vs_golden_and_safe():
     t = lambda k: torch.from_numpy(g[k])  # noqa: E731
     safe = O.moe_layer_safe(t("layer_x").to(torch.bfloat16), t("layer_w13"), t("layer_s13"),
                             t("layer_w2"), t("layer_s2"), t("layer_w"), t("layer_ids"))
-    assert_layer_parity(y, g["layer_y"], safe)
+    oracle, routes = O.moe_layer_fp64(g["layer_x"], g["layer_w13"], g["layer_s13"],
+                                      g["layer_w2"], g["layer_s2"], g["layer_w"], g["layer_ids"],
+                                      return_routes=True)
+    assert np.array_equal(oracle, g["layer_y"])
+    assert_layer_parity(y, g["layer_y"], safe, routes=routes)
 
 
 def _fp16_layer_oracle(xs, w13, s13, w2, s2, w, ids):
     """The MoE layer in float64 with the fp16 rounding points of the
-    reference composition (gate_up, silu, product, down; FP32-exact sum)."""
+    reference composition (gate_up, silu, product, down; FP32-exact sum).
+    Returns the layer output and the rounded per-route down outputs."""
     m, top_k = ids.shape
     ones = np.ones(w13.shape[0])
     gu = O.round_to_dtype(O.fused_moe_fp64(xs, w13, s13, 1.0, ones, w, ids, False,
@@ -320,7 +326,8 @@ def _fp16_layer_oracle(xs, w13, s13, w2, s2, w, ids):
     h = O.round_to_dtype(O.round_to_dtype(gg / (1 + np.exp(-gg)), "f16") * uu, "f16")
     d = O.fused_moe_fp64(h.reshape(m * top_k, inter), w2, s2, 1.0, ones, w.reshape(-1, 1),
                          ids.reshape(-1, 1), True, compute_dtype="f16")
-    return O.round_to_dtype(d, "f16")[:, 0].reshape(m, top_k, -1).sum(1)
+    routes = O.round_to_dtype(d, "f16")[:, 0].reshape(m, top_k, -1)
+    return routes.sum(1), routes
 
 
 def test_moe_layer_fp16_and_invalid_ids():
@@ -335,10 +342,11 @@ def test_moe_layer_fp16_and_invalid_ids():
     ids[5, 0] = -1
     y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
     assert y.dtype == torch.float16
-    oracle = _fp16_layer_oracle(x.float().numpy(), w13, s13, w2, s2, w.numpy(), ids.numpy())
+    oracle, routes = _fp16_layer_oracle(x.float().numpy(), w13, s13, w2, s2, w.numpy(),
+                                        ids.numpy())
     t = torch.from_numpy
     safe = O.moe_layer_safe(x, t(w13), t(s13), t(w2), t(s2), w, ids)
-    assert_layer_parity(y, oracle, safe)
+    assert_layer_parity(y, oracle, safe, routes=routes, fmt="f16")
 
 
 def test_moe_layer_fp16_multi_round_grid():
@@ -355,11 +363,12 @@ def test_moe_layer_fp16_multi_round_grid():
     y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
     rows = np.sort(np.concatenate([[17], np.random.default_rng(9).choice(m, 47, False)]))
     rows = np.unique(rows)
-    oracle = _fp16_layer_oracle(x.float().numpy()[rows], w13, s13, w2, s2, w.numpy()[rows],
-                                ids.numpy()[rows])
+    oracle, routes = _fp16_layer_oracle(x.float().numpy()[rows], w13, s13, w2, s2,
+                                        w.numpy()[rows], ids.numpy()[rows])
     t = torch.from_numpy
     safe = O.moe_layer_safe(x[rows], t(w13), t(s13), t(w2), t(s2), w[rows], ids[rows])
-    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="fp16 layer, several rounds")
+    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="fp16 layer, several rounds",
+                        routes=routes, fmt="f16")
 
 
 @pytest.mark.parametrize("m,n,k,dtype,block_m",
@@ -447,7 +456,37 @@ def test_route_topk_feeds_the_layer(layer_weights):
     assert torch.equal(ids.cpu(), tids)
     assert torch.allclose(w.cpu(), tw, rtol=2e-6, atol=0)
     y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), w, ids)
-    oracle = O.moe_layer_fp64(x.float().numpy(), w13, s13, w2, s2, tw.numpy(), tids.numpy())
+    oracle, routes = O.moe_layer_fp64(x.float().numpy(), w13, s13, w2, s2, tw.numpy(),
+                                      tids.numpy(), return_routes=True)
     t = torch.from_numpy
     safe = O.moe_layer_safe(x, t(w13), t(s13), t(w2), t(s2), tw, tids)
-    assert_layer_parity(y, oracle, safe, what="layer on device routing")
+    assert_layer_parity(y, oracle, safe, what="layer on device routing", routes=routes)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,top_k,hidden,inter", [(4, 16, 2048, 768), (3, 6, 1024, 256)],
+                         ids=["k16_two_k_waves", "k6_masked_routes"])
+def test_moe_layer_fused_decode_top_k(m, top_k, hidden, inter, dtype):
+    # the fused down + top-k kernel (<= 64 routes): top_k 16 fills four
+    # route waves and, at 512 workgroups of 16 waves, takes two K waves of
+    # up to two trips; top_k 6 leaves two of a wave's four route slots
+    # empty and takes 8-column workgroups (192 workgroups)
+    rng = np.random.default_rng(600 + top_k)
+    e = 32
+    # small scales keep every fp16 intermediate finite
+    w13, s13 = rand_mxfp4(rng, (e, 2 * inter), hidden, lo=116, hi=121)
+    w2, s2 = rand_mxfp4(rng, (e, hidden), inter, lo=116, hi=121)
+    x = rand_act(601 + top_k, (m, hidden), dtype)
+    w, ids = _route(m, e, top_k, 602 + top_k)
+    y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
+    assert y.dtype == dtype and y.shape == (m, hidden)
+    if dtype == torch.float16:
+        oracle, routes = _fp16_layer_oracle(x.float().numpy(), w13, s13, w2, s2, w.numpy(),
+                                            ids.numpy())
+    else:
+        oracle, routes = O.moe_layer_fp64(x.float().numpy(), w13, s13, w2, s2, w.numpy(),
+                                          ids.numpy(), return_routes=True)
+    t = torch.from_numpy
+    safe = O.moe_layer_safe(x, t(w13), t(s13), t(w2), t(s2), w, ids)
+    assert_layer_parity(y, oracle, safe, what=f"fused decode top_k={top_k} {dtype}",
+                        routes=routes, fmt="f16" if dtype == torch.float16 else "bf16")

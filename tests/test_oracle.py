@@ -393,3 +393,59 @@ def test_router_oracle_pinned():
     brute = sorted(range(6), key=lambda e: (-t[0, e], e))[:4]
     assert it[0].tolist() == brute == [1, 2, 4, 0]
     assert wt[0, 0] == wt[0, 1] == wt[0, 2] and abs(wt.sum() - 1.0) < 1e-15
+
+
+def test_moe_oracle_predequantized_path_and_ieee_specials():
+    # the b_values / w13_values / w2_values hooks give the default results
+    # bit for bit; with +-inf weights (E8M0 254) the oracle's library matmul
+    # gives the IEEE outcome of the exact product sum (0 * inf and
+    # inf - inf are NaN, a lone inf keeps its sign), checked against
+    # products summed elementwise
+    g = np.load(os.path.join(GOLDEN, "small_cases.npz"))
+    args = (g["layer_x"], g["layer_w13"], g["layer_s13"], g["layer_w2"], g["layer_s2"],
+            g["layer_w"], g["layer_ids"])
+    v13 = lambda e: O.dequant_values(g["layer_w13"][e], g["layer_s13"][e], "bf16")  # noqa: E731
+    v2 = lambda e: O.dequant_values(g["layer_w2"][e], g["layer_s2"][e], "bf16")  # noqa: E731
+    assert np.array_equal(O.moe_layer_fp64(*args, w13_values=v13, w2_values=v2), g["layer_y"])
+    rng = np.random.default_rng(254)
+    k, n, m = 64, 24, 5
+    codes = np.zeros((2, n, k), dtype=np.uint8)
+    codes[:, :, 7] = 4          # +inf at s = 254 in every row, block 0 ...
+    codes[:, :12, 40] = 12      # ... -inf in block 1 of half the rows
+    codes[:, 12:, 33] = 1       # ... the finite 2^126 in the other half
+    scales = np.full((2, n, k // 32), 254, dtype=np.uint8)
+    packed = O.pack_codes(codes)
+    a = rng.standard_normal((m, k))
+    a[0, 7] = 0.0               # 0 * inf
+    ids = np.array([[0, 1]] * m)
+    w = np.ones((m, 2))
+    got = O.fused_moe_fp64(a, packed, scales, 1.0, np.ones(2), w, ids, False)
+    for e in range(2):
+        wv = O.dequant_values(packed[e], scales[e], "bf16")
+        brute = (a[:, None, :] * wv[None, :, :]).sum(-1)
+        np.testing.assert_array_equal(got[:, e], brute)
+    assert np.all(np.isnan(got[0]))  # 0 * inf
+    # rows with +inf and -inf: NaN exactly where the two activations agree in sign
+    same = np.sign(a[1:, 7]) == np.sign(a[1:, 40])
+    assert np.array_equal(np.isnan(got[1:, :, :12]), np.broadcast_to(same[:, None, None],
+                                                                     (m - 1, 2, 12)))
+    assert np.array_equal(got[1:, :, 12:], np.broadcast_to(
+        (np.sign(a[1:, 7]) * np.inf)[:, None, None], (m - 1, 2, n - 12)))
+
+
+def test_format_ulp_is_the_grid_spacing():
+    # the gap to the next representable value, from the bit patterns
+    rng = np.random.default_rng(7)
+    b16 = rng.integers(0, 0x7F7F, 4000, dtype=np.uint16)  # finite positive bf16, below max
+    v = O.bf16_bits_to_f32(b16).astype(np.float64)
+    nxt = O.bf16_bits_to_f32(b16 + 1).astype(np.float64)
+    np.testing.assert_array_equal(O.format_ulp(v, "bf16"), nxt - v)
+    np.testing.assert_array_equal(O.format_ulp(-v, "bf16"), nxt - v)
+    h = rng.integers(0, 0x7BFF, 4000, dtype=np.uint16).view(np.float16)
+    np.testing.assert_array_equal(O.format_ulp(h, "f16"),
+                                  np.nextafter(h, np.float16(np.inf)).astype(np.float64) - h)
+    f = rng.integers(0, 0x7F7FFFFF, 4000, dtype=np.uint32).view(np.float32)
+    np.testing.assert_array_equal(O.format_ulp(f, "f32"),
+                                  np.nextafter(f, np.float32(np.inf)).astype(np.float64) - f)
+    assert O.format_ulp(np.array([0.0]), "bf16")[0] == 2.0 ** -133
+    assert O.format_ulp(np.array([np.nan, np.inf]), "bf16").tolist() == [0.0, 0.0]
