@@ -193,6 +193,25 @@ int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hidden, const
                     int top_k, void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * mxfp4_moe_layer without a workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * The layer's workspace is a fixed device array of
+ * MXFP4_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs
+ * on until the process ends; nothing is allocated per call.  Returns
+ * MXFP4_ERR_VALUE when mxfp4_moe_layer_workspace_size exceeds that size
+ * (at the BASELINE shape, E=128 top-8 hidden 2048 inter 768, up to ~700
+ * tokens).  Calls that overlap on one GPU share the array and race: issue
+ * them on one stream, or order them.  Otherwise as mxfp4_moe_layer.
+ */
+#define MXFP4_NOALLOC_SCRATCH_BYTES (32LL << 20)
+int mxfp4_moe_layer_noalloc(const void* x, int x_dtype, int64_t m, int64_t hidden,
+                            const uint8_t* w13, const uint8_t* s13, const uint8_t* w2,
+                            const uint8_t* s2, int num_experts, int64_t inter,
+                            const float* topk_weights, const void* topk_ids, int ids_dtype,
+                            int top_k, void* out, void* stream);
+
+/*
  * MXFP4 activation quantizer (the step before W4A4).  x [rows, k] (BF16,
  * F16 or F32, row stride in elements) -> packed u8 [rows, k/2] and
  * scales u8 [rows, k/32], contiguous.  mode MXFP4_QUANT_TIES_AWAY

@@ -16,6 +16,8 @@
 // The result is identical to the host loop of vllm:119-146 (ascending
 // experts, ascending route ids inside an expert) for ids in [0, E); other ids
 // are dropped, leaving those rows untouched (soft:476-481: they stay zero).
+#include <mutex>
+
 #include "gemm.h"
 
 namespace mx {
@@ -803,4 +805,69 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
                                                         static_cast<_Float16*>(out));
   }
   return launch_status("moe topk sum launch");
+}
+
+// ---------------------------------------------------------------- allocation-free layer
+// mxfp4_moe_layer for callers that cannot allocate device memory (code under
+// HIP graph capture, serving loops, harnesses that forbid hipMalloc): the
+// layer's workspace -- routing metadata and the h / d intermediates -- is a
+// file-scope device array of kNoAllocScratchBytes, which every GPU the
+// library runs on holds until the process ends.  The host side never uses
+// the array's name as an address: its device address is looked up once per
+// device (hipGetSymbolAddress, with that device current) and kept here.
+// No kernel of the layer needs its workspace cleared: every word a kernel
+// reads was written earlier in the same call (the routing counts per chunk,
+// h and d for every route the later kernels read).  Calls that overlap on
+// one GPU share the array and race.
+
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = MXFP4_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device); nullptr with the error set on failure.
+void* scratch_on_current_device() {
+  int dev = -1;
+  if (hip_status(hipGetDevice(&dev), "hipGetDevice") != MXFP4_OK) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("moe layer (no-alloc): device %d out of range", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)") !=
+        MXFP4_OK)
+      return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int mxfp4_moe_layer_noalloc(const void* x, int x_dtype, int64_t m, int64_t hidden,
+                                       const uint8_t* w13, const uint8_t* s13, const uint8_t* w2,
+                                       const uint8_t* s2, int num_experts, int64_t inter,
+                                       const float* topk_weights, const void* topk_ids,
+                                       int ids_dtype, int top_k, void* out, void* stream) {
+  int64_t need = 0;
+  int rc = mxfp4_moe_layer_workspace_size(m, top_k, num_experts, hidden, inter, &need);
+  if (rc) return rc;
+  if (need > kNoAllocScratchBytes) {
+    set_error("moe layer (no-alloc): %lld tokens x top-%d need a %lld-byte workspace, above the "
+              "%lld bytes of the fixed scratch; use mxfp4_moe_layer with a workspace",
+              (long long)m, top_k, (long long)need, (long long)kNoAllocScratchBytes);
+    return MXFP4_ERR_VALUE;
+  }
+  void* ws = scratch_on_current_device();
+  if (ws == nullptr) return MXFP4_ERR_HIP;
+  return mxfp4_moe_layer(x, x_dtype, m, hidden, w13, s13, w2, s2, num_experts, inter,
+                         topk_weights, topk_ids, ids_dtype, top_k, out, ws, kNoAllocScratchBytes,
+                         stream);
 }

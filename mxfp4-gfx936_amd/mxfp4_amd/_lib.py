@@ -52,6 +52,8 @@ SIGNATURES = {
     "mxfp4_moe_layer_workspace_size": [_I64, _I, _I, _I64, _I64, _P],
     "mxfp4_moe_layer": [_P, _I, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _P, _I, _I, _P, _P,
                         _I64, _P],
+    "mxfp4_moe_layer_noalloc": [_P, _I, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _P, _I, _I,
+                                _P, _P],
     "mxfp4_quant": [_P, _I, _I64, _I64, _I64, _I, _P, _P, _P],
 }
 
