@@ -56,7 +56,27 @@ struct GemmArgs {
   // FP32 to splitk_ws + s * m * n, then summed by splitk_reduce.
   float* splitk_ws;
   int32_t splitk;
+  // Optional prepacked copy of the weights (prepack.hip), read by the
+  // direct-to-LDS prefill kernels instead of b / bs: pre_b = fragment-ordered
+  // nibbles [E][G][K/64][512 B], pre_s = FP32 scale operands
+  // [E][G][K/64][16 rows][2]; G = 16-row groups; per-expert byte strides.
+  const uint8_t* pre_b;
+  const float* pre_s;
+  int64_t pre_b_e, pre_s_e;
+  // set on the copy a prefill kernel receives: b / bs / b_e / bs_e are then
+  // the prepacked arrays
+  int32_t prepacked;
 };
+
+// Bytes of the prepacked layout of `experts` weight matrices of `rows` x k
+// (k % 64 == 0): nibble blocks, then scale operands.
+__host__ __device__ inline int64_t prepacked_groups(int64_t rows) { return (rows + 15) / 16; }
+__host__ __device__ inline int64_t prepacked_nibble_bytes(int64_t rows, int64_t k) {
+  return prepacked_groups(rows) * (k / 64) * 512;
+}
+__host__ __device__ inline int64_t prepacked_scale_bytes(int64_t rows, int64_t k) {
+  return prepacked_groups(rows) * (k / 64) * 128;
+}
 
 // Per-row routing lookup used by every kernel.
 struct RowInfo {
@@ -142,6 +162,8 @@ enum PfConfig {
   PF_128x320 = 4,  // 1 x 4 waves of 128 x 80 (plain store epilogue only)
 };
 bool pf_supported(const GemmArgs& g, int elem_bytes);
+// The prepacked weights of g (pre_b / pre_s) can replace b / bs.
+bool pf_prepacked_usable(const GemmArgs& g);
 // Compute units of the current device (cached per device; 0 if unknown).
 int device_cus();
 int pf_choose(const GemmArgs& g, int epi);

@@ -53,25 +53,39 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
 }
 
-template <int WGM, int WGN, int FM, int FN, int STAGES>
+template <int WGM, int WGN, int FM, int FN, int STAGES, bool PRE = false>
 struct PfShape {
   static constexpr int NW = WGM * WGN;  // waves
   static constexpr int NT = 64 * NW;    // threads
   static constexpr int BM = WGM * FM * 16;
   static constexpr int BN = WGN * FN * 16;
+  static constexpr int GRP = BN / 16;       // 16-row weight groups
   static constexpr int A_STAGE = BM * 128;  // BM rows x 64 elements x 2 bytes
   static constexpr int B_STAGE = BN * 32;   // BN rows x 64 nibbles
   static constexpr int A_TOT = BM / 8;      // 1 KB wave-loads per stage (8 rows each)
   static constexpr int B_TOT = BN / 32;     // (32 rows each)
-  static constexpr int S_TOT = (BN + 63) / 64;  // scale wave-loads (64 rows x 4 bytes)
+  // Scales.  Original layout: the 4 E8M0 bytes of a weight row's 128 K,
+  // staged every other stage (a slot per stage pair), 4-byte lanes.
+  // Prepacked: the FP32 scale operands of a row's two 32-blocks of the
+  // stage (128 bytes per group), every stage, in 16-byte lanes, or 4-byte
+  // lanes for 3+ stages (every wave then issues the same number of loads
+  // per stage, which the partial vmcnt waits count on).
+  static constexpr int S_LANE = (PRE && STAGES == 2) ? 16 : 4;
+  static constexpr int S_BYTES = PRE ? GRP * 128 : BN * 4;
+  static constexpr int S_TOT = (S_BYTES + 64 * S_LANE - 1) / (64 * S_LANE);
   static constexpr int S_PER = (S_TOT + NW - 1) / NW;
   static constexpr int A_PER = (A_TOT + NW - 1) / NW;
   static constexpr int B_PER = (B_TOT + NW - 1) / NW;
-  static constexpr bool EVEN = A_TOT % NW == 0 && B_TOT % NW == 0;
-  static constexpr int S_SLOT = S_TOT * 256;  // 4 scale bytes (128 K) per row
-  // scale slots: one per stage pair, enough for every pair in flight
-  static constexpr int S_SLOTS = (STAGES + 2) / 2;
+  static constexpr bool EVEN =
+      A_TOT % NW == 0 && B_TOT % NW == 0 && (!PRE || S_TOT % NW == 0);
+  static constexpr int S_SLOT = S_TOT * 64 * S_LANE;
+  // scale slots: one per stage (prepacked) or stage pair, enough for every
+  // stage in flight
+  static constexpr int S_SLOTS = PRE ? STAGES : (STAGES + 2) / 2;
   static constexpr int PIPE = STAGES * (A_STAGE + B_STAGE) + S_SLOTS * S_SLOT;
+  // loads a wave issues for one stage (the prepacked scales come every stage;
+  // the original ones every other, which waiting for this count covers)
+  static constexpr int PER_STAGE = A_PER + B_PER + (PRE ? S_PER : 0);
 };
 
 // The finished tile is staged in LDS (reusing the pipeline buffers) in as
@@ -88,31 +102,51 @@ constexpr int epi_passes(int bm, int row_bytes, int pipe_bytes) {
 // then per ks: decode every weight fragment, then the FM x FN MFMAs back to
 // back.  Logical chunk ks*4 + grp of an A row sits at physical chunk (grp ^
 // sw) ^ (ks*4): flipping bit 6 of the byte offset selects the ks = 1 half.
-// Ss points at the stage's two scale bytes of the wave's first weight row.
-template <typename T, int FM, int FN>
+// Original weights: Ss points at the stage's two scale bytes of the wave's
+// first weight row, each fragment is a dword of its row (b_rd, b_sw swizzle).
+// Prepacked (PRE): a fragment's two dwords (ks = 0, 1) are 8 consecutive
+// bytes per lane of its group's 512-byte block (b_rd = group block + 8 *
+// lane), and its two scale operands 8 consecutive bytes of the group's
+// 128-byte scale block (s_rd = group block + 8 * row): conflict-free
+// 8-byte reads, no scale arithmetic.
+template <typename T, int FM, int FN, bool PRE>
 __device__ __forceinline__ void stage_math(const uint8_t* As, const uint8_t* Bs, const uint8_t* Ss,
                                            int a_rd0, int b_rd, int b_sw, int s_rd,
                                            f32x4 (&acc)[FM][FN]) {
   typedef typename V8Of<T>::type V8;
   V8 af[2][FM];
   uint32_t raw[2][FN];
-  uint32_t sb[2][FN];
+  float sc[2][FN];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
       af[ks][fm] = *reinterpret_cast<const V8*>(As + ((a_rd0 + fm * 16 * 128) ^ (ks * 64)));
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-      raw[ks][fn] = *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 16 * 32 + ((ks ^ b_sw) * 16));
-      sb[ks][fn] = Ss[s_rd + fn * 16 * 4 + ks];
+  for (int fn = 0; fn < FN; ++fn) {
+    if constexpr (PRE) {
+      // (written as dword reads, which the compiler pairs into 8-byte reads:
+      // through a uint2 / float2 type the reads lose the LDS alias
+      // information that lets them run while the next stage's direct-to-LDS
+      // loads are in flight, and a full vmcnt wait precedes them)
+      raw[0][fn] = *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 512);
+      raw[1][fn] = *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 512 + 4);
+      sc[0][fn] = *reinterpret_cast<const float*>(Ss + s_rd + fn * 128);
+      sc[1][fn] = *reinterpret_cast<const float*>(Ss + s_rd + fn * 128 + 4);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        raw[ks][fn] =
+            *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 16 * 32 + ((ks ^ b_sw) * 16));
+        sc[ks][fn] = e8m0_scale(Ss[s_rd + fn * 16 * 4 + ks]);
+      }
     }
   }
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     V8 bf[FN];
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) bf[fn] = Decode<T>::run(raw[ks][fn], e8m0_scale(sb[ks][fn]));
+    for (int fn = 0; fn < FN; ++fn) bf[fn] = Decode<T>::run(raw[ks][fn], sc[ks][fn]);
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
@@ -120,9 +154,9 @@ __device__ __forceinline__ void stage_math(const uint8_t* As, const uint8_t* Bs,
   }
 }
 
-template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB>
+template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB, bool PRE>
 __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int nbm, int nbn) {
-  typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
+  typedef PfShape<WGM, WGN, FM, FN, STAGES, PRE> S;
   constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
   constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int ES = (EPI == EPI_PARTIAL) ? 4 : 2;  // bytes per output element
@@ -133,7 +167,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   static_assert(BN % 32 == 0 && EPI_ROWS % 16 == 0, "tile config");
   static_assert(STAGES == 2 || S::EVEN, "multi-stage waits count loads per wave");
   static_assert(STAGES >= 2 && STAGES <= 8, "2 to 8 stages");
-  static_assert((STAGES - 2) * (S::A_PER + S::B_PER) <= 63, "vmcnt holds at most 63");
+  static_assert((STAGES - 2) * S::PER_STAGE <= 63, "vmcnt holds at most 63");
   static_assert(EPI != EPI_SILU_MUL || FN % 2 == 0, "SiLU pairs need even FN");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
   uint8_t* const sA = smem;
@@ -175,8 +209,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   // ---- buffer resources
   const i32x4 rA = make_rsrc(g.a, (uint32_t)(g.a_rows * g.lda * (int64_t)sizeof(T)));
   const int64_t b_rows_total = (EPI == EPI_SILU_MUL) ? 2 * (int64_t)g.inter : (int64_t)g.n;
-  const i32x4 rB = make_rsrc(g.b + expert * g.b_e, (uint32_t)(b_rows_total * g.b_n));
-  const i32x4 rS = make_rsrc(g.bs + expert * g.bs_e, (uint32_t)(b_rows_total * g.bs_n));
+  const i32x4 rB = make_rsrc(g.b + expert * g.b_e,
+                             (uint32_t)(PRE ? prepacked_nibble_bytes(b_rows_total, g.k)
+                                            : b_rows_total * g.b_n));
+  const i32x4 rS = make_rsrc(g.bs + expert * g.bs_e,
+                             (uint32_t)(PRE ? prepacked_scale_bytes(b_rows_total, g.k)
+                                            : b_rows_total * g.bs_n));
+  const int64_t nk_all = g.k / 64;  // stages of the whole K (prepacked group stride)
 
   // B-tile row -> weight row (or -1 past N).  With SiLU, 16-row blocks
   // alternate gate (even) and up (odd) rows of the same output columns.
@@ -210,21 +249,37 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
       if (ri.valid) a_off[j] = (uint32_t)(ri.a_row * g.lda * (int64_t)sizeof(T)) + c * 16;
     }
   }
+  // Prepacked: B wave-load q holds groups 2q and 2q + 1 (lanes 0-31, 32-63;
+  // 16 bytes each of the group's 512-byte stage block); scale byte b of the
+  // stage's scale region is byte b % 128 of group b / 128's 128-byte block.
   uint32_t b_off[S::B_PER];
 #pragma unroll
   for (int j = 0; j < S::B_PER; ++j) {
     const int q = j * S::NW + wave;
-    const int row = q * 32 + (lane >> 1);
-    const int c = (lane & 1) ^ ((row >> 3) & 1);
-    const int grow = q < S::B_TOT ? weight_row(row) : -1;
-    b_off[j] = grow >= 0 ? (uint32_t)(grow * g.b_n) + c * 16 : kOOB;
+    if constexpr (PRE) {
+      const int gt = 2 * q + (lane >> 5);
+      const int grow = (q < S::B_TOT && gt < S::GRP) ? weight_row(gt * 16) : -1;
+      b_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * nk_all * 512) + (lane & 31) * 16 : kOOB;
+    } else {
+      const int row = q * 32 + (lane >> 1);
+      const int c = (lane & 1) ^ ((row >> 3) & 1);
+      const int grow = q < S::B_TOT ? weight_row(row) : -1;
+      b_off[j] = grow >= 0 ? (uint32_t)(grow * g.b_n) + c * 16 : kOOB;
+    }
   }
   uint32_t s_off[S::S_PER];
 #pragma unroll
   for (int j = 0; j < S::S_PER; ++j) {
     const int q = j * S::NW + wave;
-    const int grow = q < S::S_TOT ? weight_row(q * 64 + lane) : -1;
-    s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
+    if constexpr (PRE) {
+      const int sb = (q * 64 + lane) * S::S_LANE;
+      const int gt = sb >> 7;
+      const int grow = (q < S::S_TOT && gt < S::GRP) ? weight_row(gt * 16) : -1;
+      s_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * nk_all * 128) + (sb & 127) : kOOB;
+    } else {
+      const int grow = q < S::S_TOT ? weight_row(q * 64 + lane) : -1;
+      s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
+    }
   }
 
   // 64-deep stages [k_begin, k_end) of this workgroup's K slice; slices
@@ -237,7 +292,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   }
   auto issue = [&](int kt) {
     const int st = kt % STAGES;
-    if ((kt & 1) == 0) {
+    if constexpr (PRE) {
+#pragma unroll
+      for (int j = 0; j < S::S_PER; ++j) {
+        const int q = j * S::NW + wave;
+        if (S::S_TOT % S::NW == 0 || q < S::S_TOT)
+          llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + st * S::S_SLOT + q * 64 * S::S_LANE),
+                                          S::S_LANE, (int)s_off[j], kt * 128, 0, 0);
+      }
+    } else if ((kt & 1) == 0) {
 #pragma unroll
       for (int j = 0; j < S::S_PER; ++j) {
         const int q = j * S::NW + wave;
@@ -258,7 +321,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
       const int q = j * S::NW + wave;
       if (S::B_TOT % S::NW == 0 || q < S::B_TOT)
         llvm_amdgcn_raw_buffer_load_lds(rB, lds_ptr(sB + st * S::B_STAGE + q * 1024), 16,
-                                        (int)b_off[j], kt * 32, 0, 0);
+                                        (int)b_off[j], kt * (PRE ? 512 : 32), 0, 0);
     }
   };
 
@@ -268,6 +331,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   const int b_sw = (c16 >> 3) & 1;
   const int b_rd = (wn * FN * 16 + c16) * 32 + grp * 4;
   const int s_rd = (wn * FN * 16 + c16) * 4;
+  const int b_rd_pre = wn * FN * 512 + lane * 8;  // group wn*FN's block, lane's 8 bytes
+  const int s_rd_pre = wn * FN * 128 + c16 * 8;   // group wn*FN's scales, row c16
 
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -287,18 +352,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     // outstanding.  A bare s_barrier (not __syncthreads, whose release fence
     // would drain every outstanding load) then publishes it to all waves and
     // retires the reads of the buffer the next issue() overwrites.
-    // (a wave's loads of one later stage number at most PER_STAGE, plus
-    // one scale load on even stages, which waiting for PER_STAGE covers)
-    constexpr int PER_STAGE = S::A_PER + S::B_PER;
+    // (a wave's loads of one later stage number at most PER_STAGE, plus,
+    // original layout, one scale load on even stages, which waiting for
+    // PER_STAGE covers)
     const int later = (k_end - 1 - kt) < (STAGES - 2) ? (k_end - 1 - kt) : (STAGES - 2);
     static_for<0, STAGES - 1>([&](auto c) {
-      if (later == decltype(c)::value) wait_vmcnt<decltype(c)::value * PER_STAGE>();
+      if (later == decltype(c)::value) wait_vmcnt<decltype(c)::value * S::PER_STAGE>();
     });
     barrier_only();
     if (kt + STAGES - 1 < k_end) issue(kt + STAGES - 1);
-    stage_math<T, FM, FN>(sA + (kt % STAGES) * S::A_STAGE, sB + (kt % STAGES) * S::B_STAGE,
-                          sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2, a_rd0, b_rd,
-                          b_sw, s_rd, acc);
+    if constexpr (PRE)
+      stage_math<T, FM, FN, true>(sA + (kt % STAGES) * S::A_STAGE, sB + (kt % STAGES) * S::B_STAGE,
+                                  sS + (kt % STAGES) * S::S_SLOT, a_rd0, b_rd_pre, 0, s_rd_pre, acc);
+    else
+      stage_math<T, FM, FN, false>(sA + (kt % STAGES) * S::A_STAGE, sB + (kt % STAGES) * S::B_STAGE,
+                                   sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2, a_rd0,
+                                   b_rd, b_sw, s_rd, acc);
   }
 
   // ---- epilogue: lane owns row wm*FM*16 + fm*16 + c16 and columns
@@ -435,10 +504,10 @@ extern "C" __device__ void llvm_amdgcn_raw_buffer_store_v2i32(i32x2 vdata, i32x4
                                                               int aux)
     __asm("llvm.amdgcn.raw.buffer.store.v2i32");
 
-template <typename T, int FM, int FN, int EPI, int MINB>
+template <typename T, int FM, int FN, int EPI, int MINB, bool PRE>
 __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int nbn,
                                                       uint32_t c_bytes) {
-  typedef PfShape<1, 4, FM, FN, 2> S;
+  typedef PfShape<1, 4, FM, FN, 2, PRE> S;
   constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
   constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int BIAS_PER = (OUT_COLS + NT - 1) / NT;
@@ -502,8 +571,12 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
     const int ncol0_ = bn_ * OUT_COLS;
     const int e = expert_ < 0 ? 0 : expert_;
     // expert < 0: empty resources, every operand reads zero
-    rB = make_rsrc(g.b + e * g.b_e, expert_ < 0 ? 0u : (uint32_t)(b_rows_total * g.b_n));
-    rS = make_rsrc(g.bs + e * g.bs_e, expert_ < 0 ? 0u : (uint32_t)(b_rows_total * g.bs_n));
+    const int64_t b_bytes =
+        PRE ? prepacked_nibble_bytes(b_rows_total, g.k) : b_rows_total * g.b_n;
+    const int64_t s_bytes =
+        PRE ? prepacked_scale_bytes(b_rows_total, g.k) : b_rows_total * g.bs_n;
+    rB = make_rsrc(g.b + e * g.b_e, expert_ < 0 ? 0u : (uint32_t)b_bytes);
+    rS = make_rsrc(g.bs + e * g.bs_e, expert_ < 0 ? 0u : (uint32_t)s_bytes);
     auto weight_row = [&](int i) -> int {
       int orow, grow;
       if (EPI == EPI_SILU_MUL) {
@@ -525,19 +598,33 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
       a_off[j] = (ar >= 0 && expert_ >= 0) ? (uint32_t)(ar * g.lda * (int64_t)sizeof(T)) + c * 16
                                            : kOOB;
     }
+    // (prepacked addressing as in w4a16_pf)
 #pragma unroll
     for (int j = 0; j < S::B_PER; ++j) {
       const int q = j * S::NW + wave;
-      const int row = q * 32 + (lane >> 1);
-      const int c = (lane & 1) ^ ((row >> 3) & 1);
-      const int grow = q < S::B_TOT ? weight_row(row) : -1;
-      b_off[j] = grow >= 0 ? (uint32_t)(grow * g.b_n) + c * 16 : kOOB;
+      if constexpr (PRE) {
+        const int gt = 2 * q + (lane >> 5);
+        const int grow = (q < S::B_TOT && gt < S::GRP) ? weight_row(gt * 16) : -1;
+        b_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * (int64_t)nk * 512) + (lane & 31) * 16 : kOOB;
+      } else {
+        const int row = q * 32 + (lane >> 1);
+        const int c = (lane & 1) ^ ((row >> 3) & 1);
+        const int grow = q < S::B_TOT ? weight_row(row) : -1;
+        b_off[j] = grow >= 0 ? (uint32_t)(grow * g.b_n) + c * 16 : kOOB;
+      }
     }
 #pragma unroll
     for (int j = 0; j < S::S_PER; ++j) {
       const int q = j * S::NW + wave;
-      const int grow = q < S::S_TOT ? weight_row(q * 64 + lane) : -1;
-      s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
+      if constexpr (PRE) {
+        const int sb = (q * 64 + lane) * S::S_LANE;
+        const int gt = sb >> 7;
+        const int grow = (q < S::S_TOT && gt < S::GRP) ? weight_row(gt * 16) : -1;
+        s_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * (int64_t)nk * 128) + (sb & 127) : kOOB;
+      } else {
+        const int grow = q < S::S_TOT ? weight_row(q * 64 + lane) : -1;
+        s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
+      }
     }
   };
   // stage kt of the current tile into buffer gk % 2 (gk: stage counter
@@ -545,7 +632,15 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
   // have the same parity and the scale slots alternate as in w4a16_pf)
   auto issue = [&](int kt, int gk) {
     const int st = gk & 1;
-    if ((kt & 1) == 0) {
+    if constexpr (PRE) {
+#pragma unroll
+      for (int j = 0; j < S::S_PER; ++j) {
+        const int q = j * S::NW + wave;
+        if (S::S_TOT % S::NW == 0 || q < S::S_TOT)
+          llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + st * S::S_SLOT + q * 64 * S::S_LANE),
+                                          S::S_LANE, (int)s_off[j], kt * 128, 0, 0);
+      }
+    } else if ((kt & 1) == 0) {
 #pragma unroll
       for (int j = 0; j < S::S_PER; ++j) {
         const int q = j * S::NW + wave;
@@ -566,7 +661,7 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
       const int q = j * S::NW + wave;
       if (S::B_TOT % S::NW == 0 || q < S::B_TOT)
         llvm_amdgcn_raw_buffer_load_lds(rB, lds_ptr(sB + st * S::B_STAGE + q * 1024), 16,
-                                        (int)b_off[j], kt * 32, 0, 0);
+                                        (int)b_off[j], kt * (PRE ? 512 : 32), 0, 0);
     }
   };
 
@@ -574,6 +669,8 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
   const int b_sw = (c16 >> 3) & 1;
   const int b_rd = (wave * FN * 16 + c16) * 32 + grp * 4;
   const int s_rd = (wave * FN * 16 + c16) * 4;
+  const int b_rd_pre = wave * FN * 512 + lane * 8;
+  const int s_rd_pre = wave * FN * 128 + c16 * 8;
   const i32x4 rC = make_rsrc(g.c, c_bytes);
 
   f32x4 acc[FM][FN];
@@ -598,9 +695,13 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
     for (int i = 0; i < BIAS_PER; ++i) biasv[i] = 0.f;
     // stage gk of the tile's buffer pair -> MFMAs
     auto math = [&]() {
-      stage_math<T, FM, FN>(sA + (gk & 1) * S::A_STAGE, sB + (gk & 1) * S::B_STAGE,
-                            sS + ((gk >> 1) & 1) * S::S_SLOT + (gk & 1) * 2, a_rd0, b_rd, b_sw,
-                            s_rd, acc);
+      if constexpr (PRE)
+        stage_math<T, FM, FN, true>(sA + (gk & 1) * S::A_STAGE, sB + (gk & 1) * S::B_STAGE,
+                                    sS + (gk & 1) * S::S_SLOT, a_rd0, b_rd_pre, 0, s_rd_pre, acc);
+      else
+        stage_math<T, FM, FN, false>(sA + (gk & 1) * S::A_STAGE, sB + (gk & 1) * S::B_STAGE,
+                                     sS + ((gk >> 1) & 1) * S::S_SLOT + (gk & 1) * 2, a_rd0, b_rd,
+                                     b_sw, s_rd, acc);
     };
     // Every stage: wait until stage gk has landed (nothing later is in
     // flight), then a barrier publishes it and retires the reads of the
@@ -736,9 +837,9 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
   }
 }
 
-template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB>
+template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB, bool PRE>
 int launch_cfg(const GemmArgs& g, hipStream_t st) {
-  typedef PfShape<WGM, WGN, FM, FN, STAGES> S;
+  typedef PfShape<WGM, WGN, FM, FN, STAGES, PRE> S;
   const int out_cols = (EPI == EPI_SILU_MUL) ? S::BN / 2 : S::BN;
   const int nbn = (g.n + out_cols - 1) / out_cols;
   int64_t nbm = (g.m + S::BM - 1) / S::BM;
@@ -755,7 +856,7 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
     // one load round trip, not the routed two, and gain nothing)
     const int64_t c_bytes = g.num_valid * g.ldc * (int64_t)sizeof(T);
     if (g.sorted_ids && g.n % 4 == 0 && g.ldc % 4 == 0 && c_bytes < (int64_t)0x7FFFFFFF) {
-      auto kern = w4a16_pp<T, FM, FN, EPI, MINB>;
+      auto kern = w4a16_pp<T, FM, FN, EPI, MINB, PRE>;
       // same on every device of the build target; threads that race here
       // store the same value
       static std::atomic<int> per_cu_cache{-1};
@@ -773,8 +874,8 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
       }
     }
   }
-  w4a16_pf<T, WGM, WGN, FM, FN, STAGES, EPI, MINB><<<(unsigned)nwg, S::NT, 0, st>>>(g, (int)nbm,
-                                                                                    nbn);
+  w4a16_pf<T, WGM, WGN, FM, FN, STAGES, EPI, MINB, PRE><<<(unsigned)nwg, S::NT, 0, st>>>(
+      g, (int)nbm, nbn);
   return launch_status("w4a16 prefill launch");
 }
 
@@ -807,17 +908,29 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 // 4-8 stages at 32 x 128 and 5 at 64 x 128 (M = 256-1024: 0-15% slower);
 // weights prefetched 2-4 stages ahead of the activations (no gain: the
 // routed GEMMs wait on activation rows as much).
-template <typename T, int EPI>
+template <typename T, int EPI, bool PRE>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
     case PF_128x320:
-      if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2>(g, st);
-      else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2>(g, st);  // SiLU pairs need even FN
-    case PF_128x256: return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2>(g, st);
-    case PF_128x128: return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2>(g, st);
-    case PF_64x128: return launch_cfg<T, 1, 4, 4, 2, 3, EPI, 4>(g, st);
-    default: return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4>(g, st);
+      if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2, PRE>(g, st);
+      else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // SiLU pairs need even FN
+    case PF_128x256: return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);
+    case PF_128x128: return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2, PRE>(g, st);
+    case PF_64x128: return launch_cfg<T, 1, 4, 4, 2, 3, EPI, 4, PRE>(g, st);
+    default: return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4, PRE>(g, st);
   }
+}
+
+template <typename T, int EPI>
+int launch_pf_layout(const GemmArgs& g, int cfg, hipStream_t st) {
+  if (!pf_prepacked_usable(g)) return launch_pf_typed<T, EPI, false>(g, cfg, st);
+  GemmArgs p = g;
+  p.b = g.pre_b;
+  p.bs = reinterpret_cast<const uint8_t*>(g.pre_s);
+  p.b_e = g.pre_b_e;
+  p.bs_e = g.pre_s_e;
+  p.prepacked = 1;
+  return launch_pf_typed<T, EPI, true>(p, cfg, st);
 }
 
 }  // namespace
@@ -846,6 +959,17 @@ bool pf_supported(const GemmArgs& g, int elem_bytes) {
   const int64_t brows = g.inter > 0 ? 2 * (int64_t)g.inter : (int64_t)g.n;
   if (brows * g.b_n >= (int64_t)0x7FFFFFFF) return false;
   return true;
+}
+
+bool pf_prepacked_usable(const GemmArgs& g) {
+  if (g.pre_b == nullptr || g.pre_s == nullptr) return false;
+  // 16-row groups must not straddle the gate / up halves
+  if (g.inter > 0 && g.inter % 16 != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(g.pre_b) & 15) || (reinterpret_cast<uintptr_t>(g.pre_s) & 15))
+    return false;
+  const int64_t brows = g.inter > 0 ? 2 * (int64_t)g.inter : (int64_t)g.n;
+  return prepacked_nibble_bytes(brows, g.k) < (int64_t)0x7FFFFFFF &&
+         prepacked_scale_bytes(brows, g.k) < (int64_t)0x7FFFFFFF;
 }
 
 int pf_choose(const GemmArgs& g, int epi) {
@@ -880,15 +1004,15 @@ int pf_choose(const GemmArgs& g, int epi) {
 int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t st) {
   if (dtype == MXFP4_DT_BF16) {
     switch (epi) {
-      case EPI_STORE: return launch_pf_typed<__bf16, EPI_STORE>(g, cfg, st);
-      case EPI_PARTIAL: return launch_pf_typed<__bf16, EPI_PARTIAL>(g, cfg, st);
-      default: return launch_pf_typed<__bf16, EPI_SILU_MUL>(g, cfg, st);
+      case EPI_STORE: return launch_pf_layout<__bf16, EPI_STORE>(g, cfg, st);
+      case EPI_PARTIAL: return launch_pf_layout<__bf16, EPI_PARTIAL>(g, cfg, st);
+      default: return launch_pf_layout<__bf16, EPI_SILU_MUL>(g, cfg, st);
     }
   }
   switch (epi) {
-    case EPI_STORE: return launch_pf_typed<_Float16, EPI_STORE>(g, cfg, st);
-    case EPI_PARTIAL: return launch_pf_typed<_Float16, EPI_PARTIAL>(g, cfg, st);
-    default: return launch_pf_typed<_Float16, EPI_SILU_MUL>(g, cfg, st);
+    case EPI_STORE: return launch_pf_layout<_Float16, EPI_STORE>(g, cfg, st);
+    case EPI_PARTIAL: return launch_pf_layout<_Float16, EPI_PARTIAL>(g, cfg, st);
+    default: return launch_pf_layout<_Float16, EPI_SILU_MUL>(g, cfg, st);
   }
 }
 

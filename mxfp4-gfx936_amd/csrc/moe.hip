@@ -578,6 +578,15 @@ extern "C" int mxfp4_linear_w4a16_ws(const void* x, int x_dtype, int64_t m, int6
                                      int64_t x_row_stride, const uint8_t* packed,
                                      const uint8_t* scales, int64_t n, const void* bias, void* out,
                                      void* workspace, int64_t workspace_bytes, void* stream) {
+  return mxfp4_linear_w4a16_pre(x, x_dtype, m, k, x_row_stride, packed, scales, nullptr, nullptr,
+                                n, bias, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mxfp4_linear_w4a16_pre(const void* x, int x_dtype, int64_t m, int64_t k,
+                                      int64_t x_row_stride, const uint8_t* packed,
+                                      const uint8_t* scales, const uint8_t* pre_b,
+                                      const float* pre_s, int64_t n, const void* bias, void* out,
+                                      void* workspace, int64_t workspace_bytes, void* stream) {
   if (x_dtype != MXFP4_DT_BF16 && x_dtype != MXFP4_DT_F16) {
     set_error("x must be fp16 or bf16, got dtype %d", x_dtype);
     return MXFP4_ERR_TYPE;
@@ -612,6 +621,12 @@ extern "C" int mxfp4_linear_w4a16_ws(const void* x, int x_dtype, int64_t m, int6
   g.k = (int32_t)k;
   g.top_k = 1;
   g.block_m = 16;
+  if ((pre_b == nullptr) != (pre_s == nullptr)) {
+    set_error("linear: the prepacked nibbles and scales come together");
+    return MXFP4_ERR_VALUE;
+  }
+  g.pre_b = pre_b;
+  g.pre_s = pre_s;
   if (workspace != nullptr) {
     const int64_t need = splitk_ws_bytes(m, k, n);
     if (need > 0 && (workspace_bytes < need || !aligned16(workspace))) {
@@ -677,6 +692,22 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
                                const float* topk_weights, const void* topk_ids, int ids_dtype,
                                int top_k, void* out, void* workspace, int64_t workspace_bytes,
                                void* stream) {
+  return mxfp4_moe_layer_pre(x, x_dtype, m, hidden, w13, s13, nullptr, nullptr, w2, s2, nullptr,
+                             nullptr, num_experts, inter, topk_weights, topk_ids, ids_dtype, top_k,
+                             out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mxfp4_moe_layer_pre(const void* x, int x_dtype, int64_t m, int64_t hidden,
+                                   const uint8_t* w13, const uint8_t* s13, const uint8_t* pre13_b,
+                                   const float* pre13_s, const uint8_t* w2, const uint8_t* s2,
+                                   const uint8_t* pre2_b, const float* pre2_s, int num_experts,
+                                   int64_t inter, const float* topk_weights, const void* topk_ids,
+                                   int ids_dtype, int top_k, void* out, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  if ((pre13_b == nullptr) != (pre13_s == nullptr) || (pre2_b == nullptr) != (pre2_s == nullptr)) {
+    set_error("moe layer: the prepacked nibbles and scales come together");
+    return MXFP4_ERR_VALUE;
+  }
   if (x_dtype != MXFP4_DT_BF16 && x_dtype != MXFP4_DT_F16) {
     set_error("moe layer: x must be fp16 or bf16");
     return MXFP4_ERR_TYPE;
@@ -742,6 +773,10 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
   g.block_m = p.block_m;
   g.inter = (int32_t)inter;
   g.num_experts = num_experts;
+  g.pre_b = pre13_b;
+  g.pre_s = pre13_s;
+  g.pre_b_e = prepacked_nibble_bytes(2 * inter, hidden);
+  g.pre_s_e = prepacked_scale_bytes(2 * inter, hidden);
   if (direct) {
     g.sorted_ids = nullptr;
     g.expert_ids = nullptr;
@@ -775,6 +810,10 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
   g2.k = (int32_t)inter;
   g2.top_k = 1;
   g2.inter = 0;
+  g2.pre_b = pre2_b;
+  g2.pre_s = pre2_s;
+  g2.pre_b_e = prepacked_nibble_bytes(hidden, inter);
+  g2.pre_s_e = prepacked_scale_bytes(hidden, inter);
   rc = launch_w4a16(g2, x_dtype, EPI_STORE, st);
   if (rc) return rc;
 

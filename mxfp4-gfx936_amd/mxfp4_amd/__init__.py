@@ -12,7 +12,9 @@ current stream; no host synchronisation, no fallback path):
   metadata (integration/vllm/vllm_mxfp4_gfx936.py:119-146, 233-265);
   ``route_topk`` -- router logits -> the layer's top-k weights and ids;
 * ``dynamic_mxfp4_quant`` / ``linear_mxfp4_w4a4`` -- activation quantizer
-  and dense W4A4 on the block-scaled FP4 MFMA.
+  and dense W4A4 on the block-scaled FP4 MFMA;
+* ``prepack_w4a16`` -- the fragment-ordered weight copy the prefill GEMMs
+  read when given one (``prepacked=`` / ``prepacked13=``, ``prepacked2=``).
 
 ``mxfp4_amd.vllm_adapter.install()`` points vLLM's compressed-tensors MXFP4
 schemes at these operators (integration/vllm/vllm_mxfp4_gfx936.py).
@@ -28,6 +30,7 @@ from .moe_op_mxfp4_soft import (  # noqa: F401
 from .moe_op_mxfp4 import fused_moe_mxfp4  # noqa: F401
 from .moe_layer import make_routing, moe_layer, route_topk  # noqa: F401
 from .quant import dynamic_mxfp4_quant, linear_mxfp4_w4a4  # noqa: F401
+from .prepack import PrepackedWeights, prepack_w4a16  # noqa: F401
 from . import _lib  # noqa: F401
 
 __all__ = [
@@ -41,4 +44,6 @@ __all__ = [
     "make_routing_device",
     "dynamic_mxfp4_quant",
     "linear_mxfp4_w4a4",
+    "prepack_w4a16",
+    "PrepackedWeights",
 ]

@@ -55,6 +55,12 @@ SIGNATURES = {
     "mxfp4_moe_layer_noalloc": [_P, _I, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _P, _I, _I,
                                 _P, _P],
     "mxfp4_quant": [_P, _I, _I64, _I64, _I64, _I, _P, _P, _P],
+    "mxfp4_prepack_w4a16_size": [_I64, _I64, _I64, _P, _P],
+    "mxfp4_prepack_w4a16": [_P, _P, _I64, _I64, _I64, _P, _P, _P],
+    "mxfp4_linear_w4a16_pre": [_P, _I, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _I64,
+                               _P],
+    "mxfp4_moe_layer_pre": [_P, _I, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I64, _P, _P,
+                            _I, _I, _P, _P, _I64, _P],
 }
 
 _lib = None

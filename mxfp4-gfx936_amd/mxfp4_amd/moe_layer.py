@@ -27,6 +27,7 @@ import torch
 
 from . import _lib
 from .moe_op_mxfp4_soft import make_routing_device
+from .prepack import PrepackedWeights, check_prepacked
 
 
 def moe_layer(
@@ -38,12 +39,18 @@ def moe_layer(
     topk_weights: torch.Tensor,
     topk_ids: torch.Tensor,
     activation: str = "silu",
+    *,
+    prepacked13: PrepackedWeights | None = None,
+    prepacked2: PrepackedWeights | None = None,
 ) -> torch.Tensor:
     """vllm:233-265 for MXFP4 expert weights; returns [M, H] in x.dtype.
 
     x [M, H] (bf16/fp16); w13 u8 [E, 2I, H/2], w13_scale u8 [E, 2I, H/32];
     w2 u8 [E, H, I/2], w2_scale u8 [E, H, I/32]; topk_weights [M, top_k];
     topk_ids [M, top_k] int.  Slots whose id is outside [0, E) contribute 0.
+    prepacked13 / prepacked2 (keyword only; ``prepack_w4a16`` of w13 / w2)
+    let the prefill GEMMs read the fragment-ordered copies; the result is
+    bitwise the same.
     """
     if activation != "silu":
         raise NotImplementedError(f"the gfx936 MXFP4 adapter supports silu, got {activation}")
@@ -71,6 +78,8 @@ def moe_layer(
     top_k = topk_ids.shape[1]
     device = _lib.require_device(x, w13, w13_scale, w2, w2_scale, topk_weights, topk_ids)
     lib = _lib.load()
+    pre13 = check_prepacked(prepacked13, num_experts, 2 * inter, hidden, device, "moe_layer w13")
+    pre2 = check_prepacked(prepacked2, num_experts, hidden, inter, device, "moe_layer w2")
 
     xc = _lib.aligned(x)
     ids = topk_ids if topk_ids.dtype in (torch.int32, torch.int64) else topk_ids.to(torch.int64)
@@ -84,12 +93,14 @@ def moe_layer(
                                                   ctypes.byref(nbytes)))
     ws = torch.empty(nbytes.value, dtype=torch.uint8, device=device)
     with _lib.on_device(device):
-        _lib.check(lib.mxfp4_moe_layer(
+        _lib.check(lib.mxfp4_moe_layer_pre(
             _lib.ptr(xc), _lib.dtype_code(x.dtype), m, hidden, _lib.ptr(_lib.aligned(w13)),
-            _lib.ptr(w13_scale.contiguous()), _lib.ptr(_lib.aligned(w2)),
-            _lib.ptr(w2_scale.contiguous()), num_experts, inter, _lib.ptr(weights), _lib.ptr(ids),
-            _lib.dtype_code(ids.dtype), top_k, _lib.ptr(out), _lib.ptr(ws), nbytes.value,
-            _lib.stream_of(device)))
+            _lib.ptr(w13_scale.contiguous()), _lib.ptr(pre13.nibbles if pre13 else None),
+            _lib.ptr(pre13.scales if pre13 else None), _lib.ptr(_lib.aligned(w2)),
+            _lib.ptr(w2_scale.contiguous()), _lib.ptr(pre2.nibbles if pre2 else None),
+            _lib.ptr(pre2.scales if pre2 else None), num_experts, inter, _lib.ptr(weights),
+            _lib.ptr(ids), _lib.dtype_code(ids.dtype), top_k, _lib.ptr(out), _lib.ptr(ws),
+            nbytes.value, _lib.stream_of(device)))
     return out
 
 

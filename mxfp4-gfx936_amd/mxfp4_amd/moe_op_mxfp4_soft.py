@@ -24,9 +24,11 @@ import torch
 
 try:
     from . import _lib
+    from .prepack import PrepackedWeights, check_prepacked
 except ImportError:  # loaded by file path, outside its package
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     from mxfp4_amd import _lib  # type: ignore[no-redef]
+    from mxfp4_amd.prepack import PrepackedWeights, check_prepacked  # type: ignore[no-redef]
 
 # soft:12-29 (OCP E2M1 code -> value; bit 3 is the sign)
 _MXFP4_E2M1_VALUES = (
@@ -149,13 +151,17 @@ def linear_mxfp4_soft(
     packed: torch.Tensor,
     block_scales: torch.Tensor,
     bias: torch.Tensor | None = None,
+    *,
+    prepacked: PrepackedWeights | None = None,
 ) -> torch.Tensor:
     """Weight-only OCP MXFP4 linear: ``x @ dequant(packed, block_scales).T (+ bias)``.
 
     soft:310-376.  BF16/FP16 activations, FP32 accumulation, one rounding to
     x.dtype.  A bias of x's dtype and shape [N] is fused into the epilogue;
     any other bias is added afterwards with torch's promotion, as the
-    reference does (soft:374-375).
+    reference does (soft:374-375).  ``prepacked`` (keyword only; from
+    ``prepack_w4a16(packed, block_scales)``) lets the prefill kernels read
+    the fragment-ordered copy; the result is bitwise the same.
     """
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise TypeError(f"x must be fp16 or bf16, got {x.dtype}")
@@ -177,6 +183,7 @@ def linear_mxfp4_soft(
     device = _lib.require_device(x, packed, block_scales, bias)
     lib = _lib.load()
     n = packed.shape[0]
+    pre = check_prepacked(prepacked, 1, n, logical_k, device, "linear_mxfp4_soft")
     x_2d = _lib.aligned(x.reshape(-1, logical_k))
     w = _lib.aligned(packed)
     s = block_scales.contiguous()
@@ -189,10 +196,12 @@ def linear_mxfp4_soft(
         ws_bytes = _linear_workspace_bytes(lib, x_2d.shape[0], logical_k, n)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
         with _lib.on_device(device):
-            _lib.check(lib.mxfp4_linear_w4a16_ws(
+            _lib.check(lib.mxfp4_linear_w4a16_pre(
                 _lib.ptr(x_2d), _lib.dtype_code(x.dtype), x_2d.shape[0], logical_k,
-                x_2d.stride(0), _lib.ptr(w), _lib.ptr(s), n, _lib.ptr(b), _lib.ptr(output),
-                _lib.ptr(ws), ws_bytes, _lib.stream_of(device)))
+                x_2d.stride(0), _lib.ptr(w), _lib.ptr(s),
+                _lib.ptr(pre.nibbles if pre else None), _lib.ptr(pre.scales if pre else None),
+                n, _lib.ptr(b), _lib.ptr(output), _lib.ptr(ws), ws_bytes,
+                _lib.stream_of(device)))
     if bias is not None and not fuse_bias:
         output = output + bias
     return output.reshape(*input_shape[:-1], n)

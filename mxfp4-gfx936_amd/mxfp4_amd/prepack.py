@@ -1,0 +1,94 @@
+# SPDX-License-Identifier: MIT
+"""Prepacked MXFP4 weights for the prefill GEMMs.
+
+The reference accepts only the checkpoint layout (row-major nibbles and
+E8M0 bytes) and leaves kernel-friendly swizzled layouts to AITER's own
+kernels (aiter:189-205, 229-248; soft:398-399 rejects them).  Here the
+offline repack is explicit: ``prepack_w4a16`` turns (packed, block_scales)
+into a fragment-ordered copy (per 16-row group and 64-deep K step, the
+nibbles in the order the MFMA fragments are read, and the E8M0 bytes as the
+conversion instruction's FP32 scale operands), made once when the weights
+are loaded (the vLLM adapter does it in process_weights_after_loading,
+vllm:68-70).  ``linear_mxfp4_soft(..., prepacked=...)`` and
+``moe_layer(..., prepacked13=..., prepacked2=...)`` then read the copy in
+their prefill kernels; the results are bitwise equal to the checkpoint-layout
+calls.  Decode-sized calls keep using the checkpoint layout, which must stay
+allocated.
+
+A copy belongs to the weights it was made from: after they change, prepack
+again (``PrepackedWeights.matches`` checks shapes and device, not contents).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+
+@dataclass(frozen=True)
+class PrepackedWeights:
+    """Fragment-ordered copy of ``experts`` MXFP4 matrices of ``rows`` x ``k``.
+
+    nibbles: uint8 [experts * ceil(rows/16) * k/64 * 512]
+    scales:  float32 [experts * ceil(rows/16) * k/64 * 32]
+    """
+
+    nibbles: torch.Tensor
+    scales: torch.Tensor
+    experts: int
+    rows: int
+    k: int
+
+    def matches(self, experts: int, rows: int, k: int, device: torch.device) -> bool:
+        return (self.experts, self.rows, self.k) == (experts, rows, k) and \
+            self.nibbles.device == device and self.scales.device == device
+
+
+def prepack_w4a16(packed: torch.Tensor, block_scales: torch.Tensor) -> PrepackedWeights:
+    """Prepack [rows, K/2] / [rows, K/32] (dense) or [E, rows, K/2] /
+    [E, rows, K/32] (experts) uint8 weights on their GPU.  K % 64 == 0."""
+    if packed.dtype != torch.uint8 or block_scales.dtype != torch.uint8:
+        raise TypeError("packed weights and E8M0 scales must be uint8")
+    if packed.ndim not in (2, 3) or block_scales.ndim != packed.ndim:
+        raise ValueError("prepack takes [rows, K/2] or [E, rows, K/2] weights")
+    p3 = packed if packed.ndim == 3 else packed.unsqueeze(0)
+    s3 = block_scales if block_scales.ndim == 3 else block_scales.unsqueeze(0)
+    experts, rows, half_k = p3.shape
+    k = half_k * 2
+    if s3.shape != (experts, rows, k // 32):
+        raise ValueError("one E8M0 scale is required for every 32 MXFP4 values")
+    if k % 64 != 0:
+        raise ValueError(f"prepack needs K divisible by 64, got {k}")
+    if experts < 1 or rows < 1:
+        raise ValueError("prepack needs at least one row")
+    device = _lib.require_device(packed, block_scales)
+    lib = _lib.load()
+    nb, sb = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(lib.mxfp4_prepack_w4a16_size(experts, rows, k, ctypes.byref(nb), ctypes.byref(sb)))
+    nibbles = torch.empty(nb.value, dtype=torch.uint8, device=device)
+    scales = torch.empty(sb.value // 4, dtype=torch.float32, device=device)
+    w = _lib.aligned(p3)
+    s = s3.contiguous()
+    with _lib.on_device(device):
+        _lib.check(lib.mxfp4_prepack_w4a16(
+            _lib.ptr(w), _lib.ptr(s), experts, rows, k, _lib.ptr(nibbles), _lib.ptr(scales),
+            _lib.stream_of(device)))
+    return PrepackedWeights(nibbles, scales, experts, rows, k)
+
+
+def check_prepacked(pre: PrepackedWeights | None, experts: int, rows: int, k: int,
+                    device: torch.device, what: str) -> PrepackedWeights | None:
+    """Validate a caller's prepacked copy against the weights of the call."""
+    if pre is None:
+        return None
+    if not isinstance(pre, PrepackedWeights):
+        raise TypeError(f"{what}: prepacked weights must come from prepack_w4a16")
+    if not pre.matches(experts, rows, k, device):
+        raise ValueError(
+            f"{what}: prepacked copy is for {pre.experts} x {pre.rows} x {pre.k} on "
+            f"{pre.nibbles.device}, the call has {experts} x {rows} x {k} on {device}")
+    return pre

@@ -12,6 +12,12 @@ names and meaning,
   (vllm:233-265) -> ``moe_layer`` (device routing, gate_up with SiLU*mul,
   down with the route weight, top-k sum; no host synchronisation).
 
+After loading, each layer also gets a prepacked copy of its weights
+(``prepack_w4a16``: the fragment-ordered layout its prefill GEMMs read;
+bitwise-equal results) as ``layer.mxfp4_prepacked`` (dense) or
+``layer.mxfp4_prepacked13`` / ``layer.mxfp4_prepacked2`` (MoE), unless
+``MXFP4_GFX950_PREPACK=0`` or the weights are not on a GPU.
+
 Call ``install()`` before constructing ``vllm.LLM``.  ``install(dense_cls,
 moe_cls)`` patches the given classes instead of importing vLLM's (how the
 tests exercise it without vLLM).  ``MXFP4_IMPLEMENTATION`` keeps the
@@ -30,6 +36,7 @@ from torch.nn.parameter import Parameter
 
 from .moe_layer import moe_layer
 from .moe_op_mxfp4_soft import linear_mxfp4_soft
+from .prepack import prepack_w4a16
 
 MIN_VLLM = (0, 15, 0)  # vllm:24-27
 
@@ -45,18 +52,30 @@ def _implementation() -> str:
     return impl
 
 
+def _prepacked(packed, scales):
+    """The prepacked copy of loaded weights, or None where it does not apply."""
+    if os.getenv("MXFP4_GFX950_PREPACK", "1") == "0" or not packed.is_cuda:
+        return None
+    if (packed.shape[-1] * 2) % 64 != 0:
+        return None
+    return prepack_w4a16(packed, scales)
+
+
 def _dense_process_weights_after_loading(self, layer):
-    """vllm:68-70: plain frozen parameters for the packed weight and scales."""
+    """vllm:68-70: plain frozen parameters for the packed weight and scales,
+    plus their prepacked copy."""
     del self
     layer.weight_packed = Parameter(layer.weight_packed.data, requires_grad=False)
     layer.weight_scale = Parameter(layer.weight_scale.data, requires_grad=False)
+    layer.mxfp4_prepacked = _prepacked(layer.weight_packed.data, layer.weight_scale.data)
 
 
 def _dense_apply_weights(self, layer, x, bias=None, input_quant_args=None,
                          silu_quant_args=None):
     """vllm:105-116: x @ dequant(weight).T (+ bias) on the W4A16 kernels."""
     del self, input_quant_args, silu_quant_args
-    return linear_mxfp4_soft(x, layer.weight_packed, layer.weight_scale, bias)
+    return linear_mxfp4_soft(x, layer.weight_packed, layer.weight_scale, bias,
+                             prepacked=getattr(layer, "mxfp4_prepacked", None))
 
 
 def _moe_process_weights_after_loading(self, layer):
@@ -69,6 +88,8 @@ def _moe_process_weights_after_loading(self, layer):
     layer.w2_weight_scale = Parameter(layer.w2_weight_scale.data, requires_grad=False)
     delattr(layer, "w13_weight_packed")
     delattr(layer, "w2_weight_packed")
+    layer.mxfp4_prepacked13 = _prepacked(layer.w13_weight.data, layer.w13_weight_scale.data)
+    layer.mxfp4_prepacked2 = _prepacked(layer.w2_weight.data, layer.w2_weight_scale.data)
 
 
 def _moe_apply(self, layer, x, topk_weights, topk_ids, use_nn_moe=False):
@@ -78,7 +99,9 @@ def _moe_apply(self, layer, x, topk_weights, topk_ids, use_nn_moe=False):
         raise NotImplementedError(
             f"the gfx936 MXFP4 adapter supports silu, got {layer.activation}")
     return moe_layer(x, layer.w13_weight, layer.w13_weight_scale, layer.w2_weight,
-                     layer.w2_weight_scale, topk_weights, topk_ids, activation=layer.activation)
+                     layer.w2_weight_scale, topk_weights, topk_ids, activation=layer.activation,
+                     prepacked13=getattr(layer, "mxfp4_prepacked13", None),
+                     prepacked2=getattr(layer, "mxfp4_prepacked2", None))
 
 
 def _vllm_classes():

@@ -1,0 +1,102 @@
+"""GPU: the prepacked weight copy (prepack_w4a16) is the layout its numpy
+statement gives, and every prefill kernel that reads it (dense, split K,
+routed SiLU*mul, routed with route weights, persistent) returns bitwise the
+result of the checkpoint-layout call."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mxfp4_amd as mx
+
+from _helpers import cuda, prepack_layout_np, rand_act, rand_mxfp4
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("e,rows,k", [(1, 200, 256), (3, 48, 128), (2, 5, 64)])
+def test_prepack_bytes_match_layout(e, rows, k):
+    rng = np.random.default_rng(e * 1000 + rows)
+    packed, scales = rand_mxfp4(rng, (e, rows), k, lo=0, hi=255)
+    pre = mx.prepack_w4a16(cuda(packed), cuda(scales))
+    nib, sc = prepack_layout_np(packed, scales)
+    assert (pre.experts, pre.rows, pre.k) == (e, rows, k)
+    assert np.array_equal(pre.nibbles.cpu().numpy(), nib.reshape(-1))
+    assert np.array_equal(pre.scales.view(torch.int32).cpu().numpy().view(np.uint32),
+                          sc.reshape(-1))
+    # the 2D (dense) form is the one-expert case
+    if e == 1:
+        pre2 = mx.prepack_w4a16(cuda(packed[0]), cuda(scales[0]))
+        assert torch.equal(pre2.nibbles, pre.nibbles)
+        # (bit patterns: scale byte 255 is a NaN operand)
+        assert torch.equal(pre2.scales.view(torch.int32), pre.scales.view(torch.int32))
+
+
+# (m, k, n): 128 x 320 tiles (the qkv headline), 128 x 256, 64 x 128,
+# split K (o_proj at 370 tokens), 32 x 128, a ragged N (partial 16-row
+# group), the skinny decode kernel (no prefill kernel: copy unused)
+LINEAR_CASES = [(4096, 2048, 5120), (4096, 4096, 4096), (1024, 2048, 5120), (370, 4096, 2048),
+                (256, 2048, 1536), (300, 512, 200), (8, 2048, 5120)]
+
+
+@pytest.mark.parametrize("m,k,n", LINEAR_CASES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_linear_prepacked_bitwise(m, k, n, dtype):
+    print(f"linear prepacked m={m} k={k} n={n} {dtype}", flush=True)
+    rng = np.random.default_rng(m + k + n)
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    w, s = cuda(packed), cuda(scales)
+    x = cuda(rand_act(m + n, (m, k), dtype))
+    bias = cuda(rand_act(n, (n,), dtype)) if n % 3 == 0 or n == 200 else None
+    pre = mx.prepack_w4a16(w, s)
+    plain = mx.linear_mxfp4_soft(x, w, s, bias)
+    fast = mx.linear_mxfp4_soft(x, w, s, bias, prepacked=pre)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, fast)
+    assert torch.isfinite(plain).all()
+
+
+@pytest.fixture(scope="module")
+def moe_weights():
+    e, h, i = 32, 2048, 768
+    rng = np.random.default_rng(99)
+    w13, s13 = rand_mxfp4(rng, (e, 2 * i), h)
+    w2, s2 = rand_mxfp4(rng, (e, h), i)
+    w13, s13, w2, s2 = cuda(w13), cuda(s13), cuda(w2), cuda(s2)
+    return e, h, i, (w13, s13, w2, s2), (mx.prepack_w4a16(w13, s13), mx.prepack_w4a16(w2, s2))
+
+
+# 4096 tokens: persistent routed kernel for gate_up, 128 x 320 for down;
+# 512: one round of tiles; 4: the direct-routed decode path (copies unused)
+@pytest.mark.parametrize("m", [4096, 512, 4])
+@pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32])
+def test_moe_layer_prepacked_bitwise(m, ids_dtype, moe_weights):
+    print(f"moe layer prepacked m={m} ids={ids_dtype}", flush=True)
+    e, h, _, (w13, s13, w2, s2), (p13, p2) = moe_weights
+    top_k = 8
+    g = torch.Generator().manual_seed(m)
+    logits = torch.randn((m, e), generator=g)
+    tw, ti = torch.topk(torch.softmax(logits, -1), top_k, dim=-1)
+    tw = (tw / tw.sum(-1, keepdim=True)).cuda()
+    ti = ti.to(ids_dtype).cuda()
+    if m >= 512:
+        ti[::97, 3] = -1  # a few slots routed off this device
+    x = cuda(rand_act(m, (m, h)))
+    plain = mx.moe_layer(x, w13, s13, w2, s2, tw, ti)
+    fast = mx.moe_layer(x, w13, s13, w2, s2, tw, ti, prepacked13=p13, prepacked2=p2)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, fast)
+    assert torch.isfinite(plain).all()
+
+
+def test_prepacked_copy_of_other_weights_is_refused(moe_weights):
+    _, h, i, (w13, s13, w2, s2), (p13, p2) = moe_weights
+    x = cuda(rand_act(1, (16, h)))
+    tw = torch.full((16, 2), 0.5, device="cuda")
+    ti = torch.zeros((16, 2), dtype=torch.int64, device="cuda")
+    with pytest.raises(ValueError, match="prepacked copy"):
+        mx.moe_layer(x, w13, s13, w2, s2, tw, ti, prepacked13=p2, prepacked2=p13)
+    with pytest.raises(ValueError, match="prepacked copy"):
+        mx.linear_mxfp4_soft(x, w13[0], s13[0], prepacked=p13)

@@ -1,0 +1,68 @@
+"""The prepacked weight layout: its numpy statement pinned on the CPU, and
+validation of prepacked copies against the call they are passed to."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import prepack_layout_np
+from mxfp4_amd.prepack import PrepackedWeights, check_prepacked
+
+
+def test_prepack_layout_known_positions():
+    # every byte distinct enough to locate: row r, byte b -> (r * 7 + b) % 256
+    e, rows, k = 2, 20, 128
+    packed = ((np.arange(rows)[:, None] * 7 + np.arange(k // 2)[None, :]) % 256).astype(np.uint8)
+    packed = np.stack([packed, packed ^ 0xFF])
+    scales = (np.arange(rows)[:, None] + 10 * np.arange(k // 32)[None, :]).astype(np.uint8)
+    scales = np.stack([scales, scales + 1])
+    nib, sc = prepack_layout_np(packed, scales)
+    assert nib.shape == (2, 2, 2, 64, 8) and sc.shape == (2, 2, 2, 16, 2)
+    # lane 37 = quad 2, row 5 of group 1 (row 21: padding) and group 0 (row 5)
+    for ex in range(2):
+        for st in range(2):
+            got = nib[ex, 0, st, 37]
+            for j in range(2):
+                off = st * 32 + j * 16 + 2 * 4
+                assert (got[j * 4:(j + 1) * 4] == packed[ex, 5, off:off + 4]).all()
+            assert (nib[ex, 1, st, 37] == 0).all()
+            for j in range(2):
+                assert sc[ex, 0, st, 5, j] == (int(scales[ex, 5, 2 * st + j]) << 23) | 0x400000
+                assert sc[ex, 1, st, 5, j] == (127 << 23) | 0x400000
+            # group 1, row 3 = weight row 19 (live)
+            assert sc[ex, 1, st, 3, 1] == (int(scales[ex, 19, 2 * st + 1]) << 23) | 0x400000
+
+
+def test_prepack_layout_is_a_permutation():
+    # rows a multiple of 16: the nibble blocks hold every weight byte once
+    rng = np.random.default_rng(5)
+    packed = rng.integers(0, 256, size=(3, 48, 128), dtype=np.uint8)
+    scales = rng.integers(0, 256, size=(3, 48, 8), dtype=np.uint8)
+    nib, sc = prepack_layout_np(packed, scales)
+    assert np.array_equal(np.sort(nib.reshape(3, -1), axis=1), np.sort(packed.reshape(3, -1), axis=1))
+    # the scale operand's exponent field is the E8M0 byte; mantissa 0x400000
+    assert np.array_equal(np.sort((sc >> 23).reshape(3, -1), axis=1),
+                          np.sort(scales.reshape(3, -1).astype(np.uint32), axis=1))
+    assert ((sc & 0x7FFFFF) == 0x400000).all()
+    # the scale operand as a float is 2^(s - 127) for normal bytes ... and the
+    # byte-0 operand 2^-127 (a subnormal float), byte 255 NaN
+    v = sc.view(np.float32)
+    b = (sc >> 23).astype(np.int64)
+    normal = (b > 0) & (b < 255)
+    assert np.allclose(v[normal], 1.5 * np.exp2(b[normal] - 127.0), rtol=0)
+    assert np.isnan(v[b == 255]).all()
+
+
+def test_check_prepacked_rejects_mismatches():
+    pre = PrepackedWeights(torch.zeros(512, dtype=torch.uint8), torch.zeros(32), 1, 16, 64)
+    cpu = torch.device("cpu")
+    assert check_prepacked(None, 1, 16, 64, cpu, "t") is None
+    assert check_prepacked(pre, 1, 16, 64, cpu, "t") is pre
+    with pytest.raises(ValueError, match="prepacked copy is for 1 x 16 x 64"):
+        check_prepacked(pre, 1, 32, 64, cpu, "t")
+    with pytest.raises(ValueError):
+        check_prepacked(pre, 2, 16, 64, cpu, "t")
+    with pytest.raises(TypeError, match="prepack_w4a16"):
+        check_prepacked((pre.nibbles, pre.scales), 1, 16, 64, cpu, "t")

@@ -64,6 +64,18 @@ def test_dense_weights_become_frozen_parameters():
     for t in (layer.weight_packed, layer.weight_scale):
         assert isinstance(t, torch.nn.Parameter) and not t.requires_grad
     assert layer.weight_packed.dtype == torch.uint8
+    assert layer.mxfp4_prepacked is None  # CPU weights: no prepacked copy
+
+
+def test_prepacked_copy_made_for_gpu_weights_unless_disabled(monkeypatch):
+    made = []
+    monkeypatch.setattr(va, "prepack_w4a16", lambda p, s: made.append((p, s)) or "copy")
+    gpu_w = types.SimpleNamespace(is_cuda=True, shape=(64, 1024))
+    assert va._prepacked(gpu_w, "S") == "copy" and made == [(gpu_w, "S")]
+    # K = 2 * 48 = 96 is not a multiple of 64: the kernels keep the checkpoint layout
+    assert va._prepacked(types.SimpleNamespace(is_cuda=True, shape=(64, 48)), "S") is None
+    monkeypatch.setenv("MXFP4_GFX950_PREPACK", "0")
+    assert va._prepacked(gpu_w, "S") is None and len(made) == 1
 
 
 def test_moe_weights_renamed_like_the_reference():
@@ -78,21 +90,30 @@ def test_moe_weights_renamed_like_the_reference():
         t = getattr(layer, name)
         assert isinstance(t, torch.nn.Parameter) and not t.requires_grad
     assert layer.w13_weight.shape == (2, 64, 16) and layer.w2_weight.shape == (2, 32, 16)
+    assert layer.mxfp4_prepacked13 is None and layer.mxfp4_prepacked2 is None
 
 
 def test_apply_paths_call_the_operators(monkeypatch):
     calls = []
-    monkeypatch.setattr(va, "linear_mxfp4_soft", lambda *a: calls.append(("linear", a)) or "y")
+    monkeypatch.setattr(va, "linear_mxfp4_soft",
+                        lambda *a, **k: calls.append(("linear", a, k)) or "y")
     monkeypatch.setattr(va, "moe_layer",
                         lambda *a, **k: calls.append(("moe", a, k)) or "z")
     dense = types.SimpleNamespace(weight_packed="W", weight_scale="S")
     assert va._dense_apply_weights(object(), dense, "x", "b", input_quant_args=1,
                                    silu_quant_args=2) == "y"
-    assert calls[-1] == ("linear", ("x", "W", "S", "b"))
+    assert calls[-1] == ("linear", ("x", "W", "S", "b"), {"prepacked": None})
+    dense.mxfp4_prepacked = "P"  # the copy process_weights_after_loading made
+    va._dense_apply_weights(object(), dense, "x")
+    assert calls[-1] == ("linear", ("x", "W", "S", None), {"prepacked": "P"})
     moe = types.SimpleNamespace(activation="silu", w13_weight="A", w13_weight_scale="As",
                                 w2_weight="B", w2_weight_scale="Bs")
     assert va._moe_apply(object(), moe, "x", "tw", "ti", use_nn_moe=True) == "z"
-    assert calls[-1] == ("moe", ("x", "A", "As", "B", "Bs", "tw", "ti"), {"activation": "silu"})
+    assert calls[-1] == ("moe", ("x", "A", "As", "B", "Bs", "tw", "ti"),
+                         {"activation": "silu", "prepacked13": None, "prepacked2": None})
+    moe.mxfp4_prepacked13, moe.mxfp4_prepacked2 = "P13", "P2"
+    va._moe_apply(object(), moe, "x", "tw", "ti")
+    assert calls[-1][2] == {"activation": "silu", "prepacked13": "P13", "prepacked2": "P2"}
     moe.activation = "gelu"
     with pytest.raises(NotImplementedError, match="silu"):
         va._moe_apply(object(), moe, "x", "tw", "ti")
