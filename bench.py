@@ -7,7 +7,11 @@ Prints ONE JSON line.  The headline (``value``) is BASELINE config 2's
 prefill point: the dense W4A16 linear at qkv_proj shape M=4096, K=2048,
 N=5120 (bf16 activations ~N(0,1), E2M1 codes uniform 0..15, E8M0 scales
 uniform 120..128, seeded), in TFLOP/s.  A step is one
-``linear_mxfp4_soft`` call on HBM-resident inputs; K steps are timed with a
+``linear_mxfp4_soft`` call on HBM-resident inputs, with the weights'
+prepacked copy (``prepack_w4a16``, made once before timing, as the vLLM
+adapter does when the weights are loaded); the same call on the checkpoint
+layout alone is timed beside it (``roofline.checkpoint_layout_kernel_us``).
+K steps are timed with a
 device synchronisation on both sides, after W untimed warmup steps that
 follow an untimed clock ramp (RAMP_MS of back-to-back calls: MI355X takes
 ~10-15 ms of sustained work to reach its steady clocks, and every timing
@@ -176,8 +180,9 @@ def traffic_probe() -> int:
     rng = np.random.default_rng(20260810 + 1)
     (w, s), = rand_weights(rng, (n,), k)
     x = randn_bf16(20260810, (m, k))
+    pre = mx.prepack_w4a16(w, s)
     for _ in range(12):
-        mx.linear_mxfp4_soft(x, w, s)
+        mx.linear_mxfp4_soft(x, w, s, prepacked=pre)
     a = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda").fill_(1.0)
     b = torch.empty_like(a)
     for _ in range(3):
@@ -254,12 +259,13 @@ def data_probe() -> int:
     }
     res = {}
     for name, (xa, wa) in cases.items():
-        ramp_clocks(lambda: mx.linear_mxfp4_soft(xa, wa, s))
+        pre = mx.prepack_w4a16(wa, s)
+        ramp_clocks(lambda: mx.linear_mxfp4_soft(xa, wa, s, prepacked=pre))
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(300):
-            mx.linear_mxfp4_soft(xa, wa, s)
+            mx.linear_mxfp4_soft(xa, wa, s, prepacked=pre)
         e1.record()
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) / 300 * 1e3
@@ -283,7 +289,11 @@ def sweep(mx, torch, np):
             copies = max(1, min(128, (600 << 20) // wbytes)) if m <= 370 else 1
             ws = rand_weights(rng, (n,), k, copies)
             x = randn_bf16(20260811 + m, (m, k))
-            fns = [lambda p=p, s=s: mx.linear_mxfp4_soft(x, p, s) for p, s in ws]
+            # prepacked copies as loaded by the vLLM adapter (the decode
+            # kernels read the checkpoint layout; the copy serves prefill)
+            pres = [mx.prepack_w4a16(p, s) if m >= 370 else None for p, s in ws]
+            fns = [lambda p=p, s=s, q=q: mx.linear_mxfp4_soft(x, p, s, prepacked=q)
+                   for (p, s), q in zip(ws, pres)]
             if m <= 370:
                 t = time_graph(fns, replays=10)
             else:
@@ -297,7 +307,7 @@ def sweep(mx, torch, np):
                 "mfma_frac": round(fl / t / 1e9 / BF16_PEAK_TFLOPS, 4),
                 "weight_copies": copies}
             log(f"{name} m={m}: {res[f'w4a16_{name}_m{m}']}")
-            del ws
+            del ws, pres
     torch.cuda.empty_cache()
     # --- routed MoE layer (BASELINE configs 3 and 5)
     e, hidden, inter, top_k = 128, 2048, 768, 8
@@ -306,7 +316,9 @@ def sweep(mx, torch, np):
     for _ in range(3):
         (w13, s13), = rand_weights(rng, (e, 2 * inter), hidden)
         (w2, s2), = rand_weights(rng, (e, hidden), inter)
-        layer_copies.append((w13, s13, w2, s2))
+        layer_copies.append(((w13, s13, w2, s2),
+                             {"prepacked13": mx.prepack_w4a16(w13, s13),
+                              "prepacked2": mx.prepack_w4a16(w2, s2)}))
     per_expert = 2 * inter * hidden // 2 + 2 * inter * hidden // 32 + hidden * inter // 2 + \
         hidden * inter // 32
     for m in (1, 8, 32, 512, 4096):
@@ -317,7 +329,7 @@ def sweep(mx, torch, np):
         ids = ids.cuda()
         x = randn_bf16(20260816 + m, (m, hidden))
         e_active = int(torch.unique(ids).numel())
-        fns = [lambda c=c: mx.moe_layer(x, *c, w, ids) for c in layer_copies]
+        fns = [lambda c=c, q=q: mx.moe_layer(x, *c, w, ids, **q) for c, q in layer_copies]
         if m <= 512:
             t = time_graph(fns, replays=10)
         else:
@@ -539,26 +551,35 @@ def main() -> int:
     rng = np.random.default_rng(20260810 + 1)
     (w, s), = rand_weights(rng, (n,), k)
     x = randn_bf16(20260810, (m, k))
-    log(f"headline: w4a16 linear m={m} k={k} n={n}, clock ramp {RAMP_MS:.0f} ms, "
-        f"warmup {args.warmup}, steps {args.steps}")
-    ramp_clocks(lambda: mx.linear_mxfp4_soft(x, w, s))
+    pre = mx.prepack_w4a16(w, s)  # once, as at weight load
+    log(f"headline: w4a16 linear m={m} k={k} n={n} (prepacked weights), clock ramp "
+        f"{RAMP_MS:.0f} ms, warmup {args.warmup}, steps {args.steps}")
+
+    def step():
+        mx.linear_mxfp4_soft(x, w, s, prepacked=pre)
+
+    ramp_clocks(step)
     for _ in range(args.warmup):
-        mx.linear_mxfp4_soft(x, w, s)
+        step()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
     for _ in range(args.steps):
-        mx.linear_mxfp4_soft(x, w, s)
+        step()
     end.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     kernel_ms = start.elapsed_time(end) / args.steps
+    # the same call without the prepacked copy (checkpoint layout), untimed
+    # for `value`: reported beside it
+    ckpt_ms = time_eager(lambda: mx.linear_mxfp4_soft(x, w, s), args.steps, args.warmup)[1]
     flops = 2.0 * m * n * k
     value = flops / (wall_ms * 1e-3) / 1e12
     achieved = flops / (kernel_ms * 1e-3) / 1e12
-    log(f"headline: {wall_ms:.4f} ms/step wall, {kernel_ms:.4f} ms/kernel, {value:.1f} TFLOP/s")
+    log(f"headline: {wall_ms:.4f} ms/step wall, {kernel_ms:.4f} ms/kernel, {value:.1f} TFLOP/s; "
+        f"checkpoint layout {ckpt_ms:.4f} ms/kernel")
 
     out = {
         "metric": METRIC,
@@ -575,12 +596,15 @@ def main() -> int:
         "data": "synthetic (seeded: E2M1 codes uniform 0..15, E8M0 120..128, x ~ N(0,1) bf16)",
         "config": {"workload": "w4a16_linear_qkv_prefill", "m": m, "k": k, "n": n,
                    "op": "linear_mxfp4_soft", "weights": "MXFP4 E2M1 + E8M0/32",
+                   "weight_layout": "prepacked at load (prepack_w4a16)",
                    "activations": "bf16"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                      "traffic": recorded_traffic(),
-                     "kernel": "w4a16_pf<bf16> 128x320 tile, 4 waves of 128x80 (direct-to-LDS)",
+                     "kernel": "w4a16_pf<bf16, prepacked> 128x320 tile, 4 waves of 128x80 "
+                               "(direct-to-LDS)",
                      "kernel_us": round(kernel_ms * 1e3, 3),
+                     "checkpoint_layout_kernel_us": round(ckpt_ms * 1e3, 3),
                      "algorithmic_bytes": linear_bytes(m, n, k)},
     }
     if not args.no_sweep:
