@@ -24,7 +24,8 @@ on ``bench.py --traffic-probe`` and recorded in
 profiles/w4a16_pf_qkv_prefill_traffic.md, or null when that file is absent.  ``sweep`` carries the other BASELINE points:
 decode W4A16 GEMV (HBM GB/s, weights rotated over >= 512 MB so the 256 MB
 MALL cannot serve them, launches replayed from a HIP graph), the routed MoE
-layer (us), W4A4 on the block-scaled FP4 MFMA, and the standalone dequant.
+layer (us), the soft op with C in FP32 (FP32 MFMA) and bf16, W4A4 on the
+block-scaled FP4 MFMA, and the standalone dequant.
 ``cpu_baseline`` times the reference safe path (explicit dequant +
 torch.matmul bf16, restated in oracle/) on this host's cores on a bounded
 row sample of the headline workload; ``cpu_config1`` times it on BASELINE
@@ -50,6 +51,7 @@ for _p in (ROOT, os.path.join(ROOT, "mxfp4-gfx936_amd")):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP4_PEAK_TFLOPS = 10100.0
+FP32_PEAK_TFLOPS = 157.3
 METRIC = ("W4A16 GEMM TFLOP/s (prefill) & HBM GB/s (decode), % roofline; MoE layer µs")
 
 
@@ -343,6 +345,29 @@ def sweep(mx, torch, np):
         log(f"moe m={m}: {res[f'moe_layer_m{m}']}")
     del layer_copies
     torch.cuda.empty_cache()
+    # --- the soft op's FP32 compute path (C fp32, soft:405-407) on the
+    # BASELINE gate_up shape at 512 tokens, beside the same call with C bf16
+    # (each call: device routing, C zero-fill, the routed GEMM)
+    e, k, n, m = 128, 2048, 1536, 512
+    (wp, wsc), = rand_weights(np.random.default_rng(20260818), (e, n), k)
+    a = randn_bf16(20260819, (m, k))
+    g = torch.Generator().manual_seed(20260820)
+    tw, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
+    tw, ids = tw.cuda(), ids.cuda()
+    one, ones_e, empty = (torch.ones(1, device="cuda"), torch.ones(e, device="cuda"),
+                          torch.empty(0, device="cuda"))
+    for cdt, name, peak in ((torch.float32, "f32", FP32_PEAK_TFLOPS),
+                            (torch.bfloat16, "bf16", BF16_PEAK_TFLOPS)):
+        C = torch.empty((m, top_k, n), dtype=cdt, device="cuda")
+        t = time_eager(lambda: mx.fused_moe_mxfp4_soft(a, wp, C, one, ones_e, None, wsc, tw, ids,
+                                                       empty, empty, empty, True, top_k, False,
+                                                       False), 20, 3)[1]
+        fl = 2.0 * m * top_k * n * k
+        res[f"fused_moe_soft_c{name}_m{m}"] = {
+            "us": round(t * 1e3, 2), "TFLOP/s": round(fl / t / 1e9, 2),
+            "peak_frac": round(fl / t / 1e9 / peak, 4), "peak": peak}
+        log(f"fused moe soft C {name}: {res[f'fused_moe_soft_c{name}_m{m}']}")
+    del wp, wsc
     # --- W4A4, activations/weights quantized with the RNE rule
     m, k, n = 8192, 4096, 4096
     a = randn_bf16(4, (m, k))

@@ -777,38 +777,6 @@ __global__ __launch_bounds__(256) void w4a16_tiled(GemmArgs g) {
   }
 }
 
-// ---------------------------------------------------------------- FP32 compute
-// soft:405-407 allows C (and so the compute dtype) to be FP32; the reference
-// then runs an FP32 GEMM.  Weights decode exactly to FP32; activations are
-// read as TA and widened.  One thread per output, sequential FMA over K.
-template <typename TA>
-__global__ __launch_bounds__(256) void f32_gemm(GemmArgs g) {
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  const int64_t used = rows_in_use(g);
-  for (int64_t pos = blockIdx.y; pos < used; pos += gridDim.y) {
-    const RowInfo r = row_info(g, pos);
-    if (!r.valid || col >= g.n) continue;
-    const int expert = g.sorted_ids ? block_expert(g, pos) : 0;
-    float* cp = static_cast<float*>(g.c) + r.out_row * g.ldc + col;
-    if (expert < 0) {
-      *cp = 0.f;
-      continue;
-    }
-    const uint8_t* bp = g.b + expert * g.b_e + (int64_t)col * g.b_n;
-    const uint8_t* sp = g.bs + expert * g.bs_e + (int64_t)col * g.bs_n;
-    const TA* ap = static_cast<const TA*>(g.a) + r.a_row * g.lda;
-    float acc = 0.f;
-    for (int k0 = 0; k0 < g.k; k0 += 8) {
-      const bf16x8 w = Decode<__bf16>::run(*reinterpret_cast<const uint32_t*>(bp + (k0 >> 1)),
-                                           e8m0_scale(sp[k0 >> 5]));
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc = fmaf((float)ap[k0 + j], (float)w[j], acc);
-    }
-    float o = acc * scalar_alpha(g, expert);
-    if (g.route_w) o *= g.route_w[r.out_row];
-    *cp = o;
-  }
-}
 
 // ---------------------------------------------------------------- dispatch
 // Wave layout for the skinny kernel: the fewest K-splitting waves WK whose
@@ -1020,16 +988,5 @@ int launch_w4a16(const GemmArgs& g, int dtype, int epi, hipStream_t st) {
   return MXFP4_ERR_TYPE;
 }
 
-int launch_f32_reference(const GemmArgs& g, int a_dtype, hipStream_t st) {
-  const int64_t cap = g.m;
-  dim3 grid((g.n + 255) / 256, (unsigned)(cap < 65535 ? (cap > 0 ? cap : 1) : 65535));
-  switch (a_dtype) {
-    case MXFP4_DT_F32: f32_gemm<float><<<grid, 256, 0, st>>>(g); break;
-    case MXFP4_DT_BF16: f32_gemm<__bf16><<<grid, 256, 0, st>>>(g); break;
-    case MXFP4_DT_F16: f32_gemm<_Float16><<<grid, 256, 0, st>>>(g); break;
-    default: set_error("f32 gemm: unsupported activation dtype %d", a_dtype); return MXFP4_ERR_TYPE;
-  }
-  return launch_status("f32 gemm launch");
-}
 
 }  // namespace mx

@@ -95,6 +95,30 @@ def test_fused_moe_compute_dtypes(c_dtype):
     assert_parity(C, oracle, what=str(c_dtype))
 
 
+@pytest.mark.parametrize("a_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scale_range", [(116, 130), (1, 3)])
+def test_fused_moe_fp32_compute_tiled(a_dtype, scale_range):
+    # C in FP32 (soft:405-407): the FP32-MFMA tiled path over several tile
+    # rows (block_m 64 at 1200 routes over 16 experts), column tiles with a
+    # ragged tail (N = 200), a_scale / b_scale and route weights; scale
+    # bytes 1-3 make every weight an FP32 subnormal or near it (the MFMA
+    # must keep them)
+    rng = np.random.default_rng(51 + scale_range[0])
+    m, k, n, e, top_k = 300, 1024, 200, 16, 4
+    wp, ws = rand_mxfp4(rng, (e, n), k, lo=scale_range[0], hi=scale_range[1])
+    a = rand_act(52, (m, k)).to(a_dtype)
+    w, ids = _route(m, e, top_k, 53)
+    b_scale = torch.from_numpy(rng.uniform(0.5, 2.0, size=e).astype(np.float32))
+    C = torch.empty((m, top_k, n), dtype=torch.float32, device="cuda")
+    mx.fused_moe_mxfp4_soft(cuda(a), cuda(wp), C, torch.full((1,), 0.75, device="cuda"),
+                            cuda(b_scale), None, cuda(ws), cuda(w), cuda(ids),
+                            _empty(), _empty(), _empty(), True, top_k, False, False)
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 0.75, b_scale.numpy(), w.numpy(),
+                              ids.numpy(), True, compute_dtype="f32")
+    assert np.abs(oracle).max() > 0
+    assert_parity(C, oracle, what=f"{a_dtype} scales {scale_range}")
+
+
 def test_fused_moe_out_of_range_ids_stay_zero():
     rng = np.random.default_rng(43)
     m, k, n, e, top_k = 5, 128, 48, 4, 2
