@@ -163,8 +163,9 @@ __host__ __device__ __forceinline__ int stage_stride(int nunits) {
 // the end) except the activation loads of padding rows, which are
 // exec-masked off.  Routed blocks read the block's expert id and the padded
 // row count with two independent scalar loads.
-template <typename T, int RB, int WK, int WN, int CG, int U, int EPI>
+template <typename T, int RB, int WK, int WN, int CG, int U, int EPI, int SR>
 __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
+  constexpr int srows = SR;  // block rows staged through LDS
   typedef typename V8Of<T>::type V8;
   constexpr int CB = (EPI == EPI_SILU_MUL) ? 2 : 1;
   constexpr int NB = CB * CG;  // weight blocks of 16 rows per wave
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
     const bool s_dword = ((g.bs_n | g.bs_e | (int64_t)reinterpret_cast<uintptr_t>(g.bs)) & 3) == 0;
     const uint32_t sshift = s_dword ? 8u * grp : 0u;
     // Activation staging: when one trip covers K, block rows
-    // 0 .. kStageRows-1 are copied once per workgroup into LDS with
+    // 0 .. srows-1 are copied once per workgroup into LDS with
     // direct-to-LDS loads (1 KB per instruction, all lanes active) instead
     // of 16 lane-masked loads per wave; other rows load per lane.  The
     // copies are issued after the weight loads, which do not wait for the
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
       }
       if (stage) {
         const int qn = (nunits * 256 + 1023) / 1024;
-        for (int i = wave; i < kStageRows * qn; i += WK * WN) {
+        for (int i = wave; i < srows * qn; i += WK * WN) {
           const int br = i / qn, q = i - (i / qn) * qn;
           const int route = __builtin_amdgcn_readlane((int)my_route[0], br);
           if (route < 0) continue;
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
         const bool k_ok = k0 < g.k;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
-          const bool staged = stage && rb * 16 + c16 < kStageRows;
+          const bool staged = stage && rb * 16 + c16 < srows;
           // nothing in this branch consumes the loaded values, so no wait
           // is placed in it
           if (k_ok && aoff[rb] != kOOB && !staged) {
@@ -335,7 +336,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
           for (int rb = 0; rb < RB; ++rb) {
             const int br = rb * 16 + c16;
             const bool k_ok = (u0 + uu) * 128 + grp * 32 < g.k;
-            if (br < kStageRows && aoff[rb] != kOOB && k_ok) {
+            if (br < srows && aoff[rb] != kOOB && k_ok) {
               const uint8_t* src = a_lds + br * a_stride + (u0 + uu) * 256 + grp * 64;
 #pragma unroll
               for (int j = 0; j < 4; ++j) af[uu][rb][j] = *reinterpret_cast<const V8*>(src + 16 * j);
@@ -807,17 +808,39 @@ SkinnyShape skinny_shape(int64_t k, int64_t n, int64_t row_blocks, int rb) {
   return s;
 }
 
-template <typename T, int RB, int CG, int EPI>
-void skinny_launch_cg(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStream_t st) {
+// Rows of a skinny block staged through LDS (SR, a template argument: a
+// run-time count costs the M=1 GEMV ~0.4 us).  Dense single-block GEMMs of
+// 5-16 rows stage 8 or 16 rows within a 72 KB budget; routed blocks and the
+// rest stage kStageRows (routed blocks mostly hold a route or two, and the
+// larger allocation costs occupancy: MoE layer M=8 39.5 -> 40.1 us with 8).
+int skinny_stage_rows(const GemmArgs& g, int rb) {
+  if (g.sorted_ids || g.route_ids || rb != 1 || g.m <= kStageRows) return kStageRows;
+  const int64_t fit = (int64_t)(72 << 10) / stage_stride((g.k + 127) / 128);
+  if (g.m > 8 && fit >= 16) return 16;
+  return fit >= 8 ? 8 : kStageRows;
+}
+
+template <typename T, int RB, int CG, int EPI, int SR>
+void skinny_launch_sr(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStream_t st) {
   constexpr int U = RB == 1 ? 4 : 2;
   const int nunits = (g.k + 127) / 128;
-  const size_t lds = nunits <= s.wk * U ? (size_t)kStageRows * stage_stride(nunits) : 0;
+  const size_t lds = nunits <= s.wk * U ? (size_t)SR * stage_stride(nunits) : 0;
   switch (s.wk) {
-    case 1: w4a16_skinny<T, RB, 1, 4, CG, U, EPI><<<grid, 256, lds, st>>>(g); break;
-    case 2: w4a16_skinny<T, RB, 2, 2, CG, U, EPI><<<grid, 256, lds, st>>>(g); break;
-    case 4: w4a16_skinny<T, RB, 4, 1, CG, U, EPI><<<grid, 256, lds, st>>>(g); break;
-    default: w4a16_skinny<T, RB, 8, 1, CG, U, EPI><<<grid, 512, lds, st>>>(g); break;
+    case 1: w4a16_skinny<T, RB, 1, 4, CG, U, EPI, SR><<<grid, 256, lds, st>>>(g); break;
+    case 2: w4a16_skinny<T, RB, 2, 2, CG, U, EPI, SR><<<grid, 256, lds, st>>>(g); break;
+    case 4: w4a16_skinny<T, RB, 4, 1, CG, U, EPI, SR><<<grid, 256, lds, st>>>(g); break;
+    default: w4a16_skinny<T, RB, 8, 1, CG, U, EPI, SR><<<grid, 512, lds, st>>>(g); break;
   }
+}
+
+template <typename T, int RB, int CG, int EPI>
+void skinny_launch_cg(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStream_t st) {
+  const int sr = skinny_stage_rows(g, RB);
+  if constexpr (RB == 1 && EPI == EPI_STORE) {
+    if (sr == 16) return skinny_launch_sr<T, RB, CG, EPI, 16>(g, s, grid, st);
+    if (sr == 8) return skinny_launch_sr<T, RB, CG, EPI, 8>(g, s, grid, st);
+  }
+  skinny_launch_sr<T, RB, CG, EPI, kStageRows>(g, s, grid, st);
 }
 
 template <typename T, int CS, int EPI>

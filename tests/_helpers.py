@@ -140,13 +140,16 @@ def fp32_gemm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 def assert_rows_parity(y: torch.Tensor, o: torch.Tensor, ref: torch.Tensor | None = None,
-                       what: str = "", row_block: int = 1):
+                       what: str = "", row_block: int = 1, fmt: torch.dtype | None = None):
     """Whole-output parity on the device.  Elementwise relative error <=
     ELEM_TOL with the denominator floored at 1e-3 * rms of the whole output;
     norm-wise <= NORM_TOL for every block of ``row_block`` rows (1: every
     row), so a wrong tile anywhere fails; with ``ref`` (the reference safe
     path on the same inputs) every block must also be no worse than it
-    (10% slack for bf16 rounding noise)."""
+    (10% slack for bf16 rounding noise).  With ``fmt`` (the output dtype) a
+    block's norm-wise bar is no tighter than 1.1x the error of ``o``
+    correctly rounded to ``fmt``: a short row (a few hundred outputs) can
+    exceed 2e-3 from the output rounding alone."""
     y2 = y.reshape(y.shape[0], -1).double()
     o2 = o.reshape(o.shape[0], -1).double()
     rms = o2.square().mean().sqrt().item()
@@ -163,9 +166,16 @@ def assert_rows_parity(y: torch.Tensor, o: torch.Tensor, ref: torch.Tensor | Non
 
     on = block_norm(o2)
     err = block_norm(y2 - o2) / on.clamp(min=1e-300)
+    bar = torch.full_like(err, O.NORM_TOL)
+    if fmt is not None:
+        floor = block_norm(o.reshape(o.shape[0], -1).to(fmt).double() - o2) / on.clamp(min=1e-300)
+        bar = torch.maximum(bar, 1.1 * floor)
+    worst = (err / bar).max().item()
+    assert worst <= 1.0, (
+        f"{what} norm-wise {err[(err / bar).argmax()].item():.3e} (bar "
+        f"{bar[(err / bar).argmax()].item():.3e}) in block {int((err / bar).argmax())} of "
+        f"{row_block} rows")
     worst = err.max().item()
-    assert worst <= O.NORM_TOL, (
-        f"{what} norm-wise {worst:.3e} in block {int(err.argmax())} of {row_block} rows")
     if ref is not None:
         r2 = ref.reshape(ref.shape[0], -1).double()
         rerr = block_norm(r2 - o2) / on.clamp(min=1e-300)

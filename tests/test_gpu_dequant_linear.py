@@ -15,7 +15,8 @@ import mxfp4_amd as mx
 from mxfp4_amd import _lib
 from oracle import c_oracle, mxfp4_oracle as O
 
-from _helpers import assert_parity, cuda, rand_act, rand_mxfp4
+from _helpers import (assert_parity, assert_rows_parity, cuda, dequant_device, fp32_gemm,
+                      rand_act, rand_mxfp4)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::RuntimeWarning")]
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -129,6 +130,23 @@ def test_linear_wide_tile_shapes(m, k, n):
     rows = np.sort(np.concatenate([rng.choice(m, 96, replace=False), [m - 1]]))
     oracle = O.linear_fp64(x.float().numpy()[rows], packed, scales)
     assert_parity(y[rows], oracle, ref=ref[rows], what=f"linear m={m} k={k} n={n}")
+
+
+@pytest.mark.parametrize("k,n", [(2048, 512), (4096, 384), (640, 272)])
+def test_linear_decode_every_m(k, n):
+    # every dense decode size of the skinny kernel: 1-16 rows (one 16-row
+    # block, up to all of its rows staged through LDS; 8 at K=4096), 17-32
+    # (two blocks); x rows strided (a column slice of a wider tensor)
+    rng = np.random.default_rng(k + n)
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    w = dequant_device(packed, scales)
+    wp, ws = cuda(packed), cuda(scales)
+    for m in list(range(1, 17)) + [17, 24, 31, 32]:
+        xw = cuda(rand_act(m * 7 + k, (m, k + 256)))
+        x = xw[:, 128:128 + k]
+        y = mx.linear_mxfp4_soft(x, wp, ws)
+        ref = fp32_gemm(x, w)
+        assert_rows_parity(y, ref, what=f"m={m} k={k} n={n}", fmt=torch.bfloat16)
 
 
 def test_linear_rejects_k_not_multiple_of_128():
