@@ -110,19 +110,19 @@ int mxfp4_linear_w4a16_ws(const void* x, int x_dtype, int64_t m, int64_t k, int6
  * once at weight load (vllm:68-70, process_weights_after_loading).  packed
  * u8 [experts, rows, k/2] and scales u8 [experts, rows, k/32] (contiguous,
  * packed 4-byte aligned) -> pre_b [experts][ceil(rows/16)][k/64][512 B]
- * and pre_s [experts][ceil(rows/16)][k/64][16][2] F32, sizes from
+ * and pre_s [experts][ceil(rows/16)][k/64][16][2] u16, sizes from
  * mxfp4_prepack_w4a16_size, both 16-byte aligned.  Per 16-row group and
  * 64-deep K step, pre_b holds the nibbles in the order the prefill kernels
  * read their MFMA fragments (lane l: bytes s*32 + j*16 + (l/16)*4 .. +3 of
- * row l % 16, j = 0, 1) and pre_s the conversion scale operands
- * (float bits (byte << 23) | 0x400000).  Rows past `rows` are zero.
- * k % 64 == 0.  A copy is valid for the weights it was made from: after
- * they change, prepack again.
+ * row l % 16, j = 0, 1) and pre_s the high halves of the conversion scale
+ * operands ((byte << 7) | 0x40: the float (byte << 23) | 0x400000).  Rows
+ * past `rows` are zero.  k % 64 == 0.  A copy is valid for the weights it
+ * was made from: after they change, prepack again.
  */
 int mxfp4_prepack_w4a16_size(int64_t experts, int64_t rows, int64_t k, int64_t* nibble_bytes,
                              int64_t* scale_bytes);
 int mxfp4_prepack_w4a16(const uint8_t* packed, const uint8_t* scales, int64_t experts,
-                        int64_t rows, int64_t k, uint8_t* pre_b, float* pre_s, void* stream);
+                        int64_t rows, int64_t k, uint8_t* pre_b, uint16_t* pre_s, void* stream);
 
 /*
  * mxfp4_linear_w4a16_ws (soft:310-376) that also takes the prepacked copy
@@ -133,7 +133,7 @@ int mxfp4_prepack_w4a16(const uint8_t* packed, const uint8_t* scales, int64_t ex
  */
 int mxfp4_linear_w4a16_pre(const void* x, int x_dtype, int64_t m, int64_t k, int64_t x_row_stride,
                            const uint8_t* packed, const uint8_t* scales, const uint8_t* pre_b,
-                           const float* pre_s, int64_t n, const void* bias, void* out,
+                           const uint16_t* pre_s, int64_t n, const void* bias, void* out,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
@@ -231,9 +231,9 @@ int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hidden, const
  * or both set; the result is bitwise equal to mxfp4_moe_layer's.
  */
 int mxfp4_moe_layer_pre(const void* x, int x_dtype, int64_t m, int64_t hidden, const uint8_t* w13,
-                        const uint8_t* s13, const uint8_t* pre13_b, const float* pre13_s,
+                        const uint8_t* s13, const uint8_t* pre13_b, const uint16_t* pre13_s,
                         const uint8_t* w2, const uint8_t* s2, const uint8_t* pre2_b,
-                        const float* pre2_s, int num_experts, int64_t inter,
+                        const uint16_t* pre2_s, int num_experts, int64_t inter,
                         const float* topk_weights, const void* topk_ids, int ids_dtype, int top_k,
                         void* out, void* workspace, int64_t workspace_bytes, void* stream);
 

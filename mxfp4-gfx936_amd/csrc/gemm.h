@@ -58,10 +58,11 @@ struct GemmArgs {
   int32_t splitk;
   // Optional prepacked copy of the weights (prepack.hip), read by the
   // direct-to-LDS prefill kernels instead of b / bs: pre_b = fragment-ordered
-  // nibbles [E][G][K/64][512 B], pre_s = FP32 scale operands
-  // [E][G][K/64][16 rows][2]; G = 16-row groups; per-expert byte strides.
+  // nibbles [E][G][K/64][512 B], pre_s = the high halves of the FP32 scale
+  // operands [E][G][K/64][16 rows][2]; G = 16-row groups; per-expert byte
+  // strides.
   const uint8_t* pre_b;
-  const float* pre_s;
+  const uint16_t* pre_s;
   int64_t pre_b_e, pre_s_e;
   // set on the copy a prefill kernel receives: b / bs / b_e / bs_e are then
   // the prepacked arrays
@@ -75,7 +76,7 @@ __host__ __device__ inline int64_t prepacked_nibble_bytes(int64_t rows, int64_t 
   return prepacked_groups(rows) * (k / 64) * 512;
 }
 __host__ __device__ inline int64_t prepacked_scale_bytes(int64_t rows, int64_t k) {
-  return prepacked_groups(rows) * (k / 64) * 128;
+  return prepacked_groups(rows) * (k / 64) * 64;
 }
 
 // Per-row routing lookup used by every kernel.

@@ -66,13 +66,16 @@ struct PfShape {
   static constexpr int B_TOT = BN / 32;     // (32 rows each)
   // Scales.  Original layout: the 4 E8M0 bytes of a weight row's 128 K,
   // staged every other stage (a slot per stage pair), 4-byte lanes.
-  // Prepacked: the FP32 scale operands of a row's two 32-blocks of the
-  // stage (128 bytes per group), every stage, in 16-byte lanes, or 4-byte
-  // lanes for 3+ stages (every wave then issues the same number of loads
-  // per stage, which the partial vmcnt waits count on).
+  // Prepacked: the 16-bit scale operand halves of a row's two 32-blocks of
+  // the stage (64 bytes per group), every stage, in 16-byte lanes, or for
+  // 3+ stages in 4-byte lanes with the wave-loads rounded up to a multiple
+  // of the waves (every wave then issues the same number of loads per
+  // stage, which the partial vmcnt waits count on; the extra lanes read
+  // past the end, i.e. zeros, into the slot's unused tail).
   static constexpr int S_LANE = (PRE && STAGES == 2) ? 16 : 4;
-  static constexpr int S_BYTES = PRE ? GRP * 128 : BN * 4;
-  static constexpr int S_TOT = (S_BYTES + 64 * S_LANE - 1) / (64 * S_LANE);
+  static constexpr int S_BYTES = PRE ? GRP * 64 : BN * 4;
+  static constexpr int S_RAW = (S_BYTES + 64 * S_LANE - 1) / (64 * S_LANE);
+  static constexpr int S_TOT = (PRE && STAGES > 2) ? (S_RAW + NW - 1) / NW * NW : S_RAW;
   static constexpr int S_PER = (S_TOT + NW - 1) / NW;
   static constexpr int A_PER = (A_TOT + NW - 1) / NW;
   static constexpr int B_PER = (B_TOT + NW - 1) / NW;
@@ -106,9 +109,9 @@ constexpr int epi_passes(int bm, int row_bytes, int pipe_bytes) {
 // first weight row, each fragment is a dword of its row (b_rd, b_sw swizzle).
 // Prepacked (PRE): a fragment's two dwords (ks = 0, 1) are 8 consecutive
 // bytes per lane of its group's 512-byte block (b_rd = group block + 8 *
-// lane), and its two scale operands 8 consecutive bytes of the group's
-// 128-byte scale block (s_rd = group block + 8 * row): conflict-free
-// 8-byte reads, no scale arithmetic.
+// lane), and the high halves of its two scale operands one dword of the
+// group's 64-byte scale block (s_rd = group block + 4 * row): conflict-free
+// reads, one shift or mask per scale.
 template <typename T, int FM, int FN, bool PRE>
 __device__ __forceinline__ void stage_math(const uint8_t* As, const uint8_t* Bs, const uint8_t* Ss,
                                            int a_rd0, int b_rd, int b_sw, int s_rd,
@@ -131,8 +134,9 @@ __device__ __forceinline__ void stage_math(const uint8_t* As, const uint8_t* Bs,
       // loads are in flight, and a full vmcnt wait precedes them)
       raw[0][fn] = *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 512);
       raw[1][fn] = *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 512 + 4);
-      sc[0][fn] = *reinterpret_cast<const float*>(Ss + s_rd + fn * 128);
-      sc[1][fn] = *reinterpret_cast<const float*>(Ss + s_rd + fn * 128 + 4);
+      const uint32_t sv = *reinterpret_cast<const uint32_t*>(Ss + s_rd + fn * 64);
+      sc[0][fn] = __uint_as_float(sv << 16);
+      sc[1][fn] = __uint_as_float(sv & 0xFFFF0000u);
     } else {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -251,7 +255,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   }
   // Prepacked: B wave-load q holds groups 2q and 2q + 1 (lanes 0-31, 32-63;
   // 16 bytes each of the group's 512-byte stage block); scale byte b of the
-  // stage's scale region is byte b % 128 of group b / 128's 128-byte block.
+  // stage's scale region is byte b % 64 of group b / 64's 64-byte block.
   uint32_t b_off[S::B_PER];
 #pragma unroll
   for (int j = 0; j < S::B_PER; ++j) {
@@ -273,9 +277,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     const int q = j * S::NW + wave;
     if constexpr (PRE) {
       const int sb = (q * 64 + lane) * S::S_LANE;
-      const int gt = sb >> 7;
+      const int gt = sb >> 6;
       const int grow = (q < S::S_TOT && gt < S::GRP) ? weight_row(gt * 16) : -1;
-      s_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * nk_all * 128) + (sb & 127) : kOOB;
+      s_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * nk_all * 64) + (sb & 63) : kOOB;
     } else {
       const int grow = q < S::S_TOT ? weight_row(q * 64 + lane) : -1;
       s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
@@ -298,7 +302,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
         const int q = j * S::NW + wave;
         if (S::S_TOT % S::NW == 0 || q < S::S_TOT)
           llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + st * S::S_SLOT + q * 64 * S::S_LANE),
-                                          S::S_LANE, (int)s_off[j], kt * 128, 0, 0);
+                                          S::S_LANE, (int)s_off[j], kt * 64, 0, 0);
       }
     } else if ((kt & 1) == 0) {
 #pragma unroll
@@ -332,7 +336,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   const int b_rd = (wn * FN * 16 + c16) * 32 + grp * 4;
   const int s_rd = (wn * FN * 16 + c16) * 4;
   const int b_rd_pre = wn * FN * 512 + lane * 8;  // group wn*FN's block, lane's 8 bytes
-  const int s_rd_pre = wn * FN * 128 + c16 * 8;   // group wn*FN's scales, row c16
+  const int s_rd_pre = wn * FN * 64 + c16 * 4;    // group wn*FN's scales, row c16
 
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -618,9 +622,9 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
       const int q = j * S::NW + wave;
       if constexpr (PRE) {
         const int sb = (q * 64 + lane) * S::S_LANE;
-        const int gt = sb >> 7;
+        const int gt = sb >> 6;
         const int grow = (q < S::S_TOT && gt < S::GRP) ? weight_row(gt * 16) : -1;
-        s_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * (int64_t)nk * 128) + (sb & 127) : kOOB;
+        s_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * (int64_t)nk * 64) + (sb & 63) : kOOB;
       } else {
         const int grow = q < S::S_TOT ? weight_row(q * 64 + lane) : -1;
         s_off[j] = grow >= 0 ? (uint32_t)(grow * g.bs_n) : kOOB;
@@ -638,7 +642,7 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
         const int q = j * S::NW + wave;
         if (S::S_TOT % S::NW == 0 || q < S::S_TOT)
           llvm_amdgcn_raw_buffer_load_lds(rS, lds_ptr(sS + st * S::S_SLOT + q * 64 * S::S_LANE),
-                                          S::S_LANE, (int)s_off[j], kt * 128, 0, 0);
+                                          S::S_LANE, (int)s_off[j], kt * 64, 0, 0);
       }
     } else if ((kt & 1) == 0) {
 #pragma unroll
@@ -670,7 +674,7 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
   const int b_rd = (wave * FN * 16 + c16) * 32 + grp * 4;
   const int s_rd = (wave * FN * 16 + c16) * 4;
   const int b_rd_pre = wave * FN * 512 + lane * 8;
-  const int s_rd_pre = wave * FN * 128 + c16 * 8;
+  const int s_rd_pre = wave * FN * 64 + c16 * 4;
   const i32x4 rC = make_rsrc(g.c, c_bytes);
 
   f32x4 acc[FM][FN];

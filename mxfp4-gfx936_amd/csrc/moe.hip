@@ -585,7 +585,7 @@ extern "C" int mxfp4_linear_w4a16_ws(const void* x, int x_dtype, int64_t m, int6
 extern "C" int mxfp4_linear_w4a16_pre(const void* x, int x_dtype, int64_t m, int64_t k,
                                       int64_t x_row_stride, const uint8_t* packed,
                                       const uint8_t* scales, const uint8_t* pre_b,
-                                      const float* pre_s, int64_t n, const void* bias, void* out,
+                                      const uint16_t* pre_s, int64_t n, const void* bias, void* out,
                                       void* workspace, int64_t workspace_bytes, void* stream) {
   if (x_dtype != MXFP4_DT_BF16 && x_dtype != MXFP4_DT_F16) {
     set_error("x must be fp16 or bf16, got dtype %d", x_dtype);
@@ -699,8 +699,8 @@ extern "C" int mxfp4_moe_layer(const void* x, int x_dtype, int64_t m, int64_t hi
 
 extern "C" int mxfp4_moe_layer_pre(const void* x, int x_dtype, int64_t m, int64_t hidden,
                                    const uint8_t* w13, const uint8_t* s13, const uint8_t* pre13_b,
-                                   const float* pre13_s, const uint8_t* w2, const uint8_t* s2,
-                                   const uint8_t* pre2_b, const float* pre2_s, int num_experts,
+                                   const uint16_t* pre13_s, const uint8_t* w2, const uint8_t* s2,
+                                   const uint8_t* pre2_b, const uint16_t* pre2_s, int num_experts,
                                    int64_t inter, const float* topk_weights, const void* topk_ids,
                                    int ids_dtype, int top_k, void* out, void* workspace,
                                    int64_t workspace_bytes, void* stream) {

@@ -10,27 +10,29 @@
 //   nibbles  [E][G][K/64][64 lanes][2 dwords]   512 bytes per (g, s)
 //     lane l, dword j = bytes s*32 + j*16 + (l/16)*4 .. +3 of row g*16 + l%16
 //     (j = the stage's first / second 32-deep half)
-//   scales   [E][G][K/64][16 rows][2] float      128 bytes per (g, s)
-//     row r, j = the conversion's scale operand of E8M0 byte 2s + j of row
-//     g*16 + r (the float whose exponent field is that byte)
+//   scales   [E][G][K/64][16 rows][2] uint16     64 bytes per (g, s)
+//     row r, j = the high half of the conversion's scale operand for E8M0
+//     byte 2s + j of row g*16 + r: (byte << 7) | 0x40, i.e. the float
+//     (byte << 23) | 0x400000 without its all-zero low half
 //
-// so a fragment and its two scales are 8 consecutive bytes each in LDS: one
-// conflict-free ds_read_b64 per fragment pair, no scale arithmetic.  Rows
-// past the end of the matrix (the last group of a row count that is not a
-// multiple of 16) are zero nibbles.  Same bits in, same MFMA inputs: GEMMs
-// on the prepacked copy are bitwise equal to GEMMs on the checkpoint layout.
+// so a fragment is 8 consecutive bytes and its two scales one dword in LDS:
+// one conflict-free ds_read_b64 per fragment pair, one dword read and a
+// shift / mask per scale pair.  Rows past the end of the matrix (the last
+// group of a row count that is not a multiple of 16) are zero nibbles.
+// Same bits in, same MFMA inputs: GEMMs on the prepacked copy are bitwise
+// equal to GEMMs on the checkpoint layout.
 #include "gemm.h"
 
 namespace mx {
 namespace {
 
 // One thread per 8-byte lane slot of a nibble block; threads of lanes 0-15
-// also write their row's two scale operands.
+// also write their row's two scale operand halves.
 __global__ __launch_bounds__(256) void prepack_w4a16(const uint8_t* __restrict__ packed,
                                                      const uint8_t* __restrict__ scales,
                                                      int64_t experts, int64_t rows, int64_t k,
                                                      uint2* __restrict__ pre_b,
-                                                     float2* __restrict__ pre_s) {
+                                                     uint32_t* __restrict__ pre_s) {
   const int64_t nk = k / 64;
   const int64_t groups = prepacked_groups(rows);
   const int64_t total = experts * groups * nk * 64;
@@ -43,17 +45,19 @@ __global__ __launch_bounds__(256) void prepack_w4a16(const uint8_t* __restrict__
     const int64_t e = eg / groups;
     const int64_t row = (eg % groups) * 16 + (l & 15);
     uint2 v{0u, 0u};
-    float2 sc{e8m0_scale(127), e8m0_scale(127)};
+    uint32_t sb0 = 127, sb1 = 127;
     if (row < rows) {
       const uint8_t* wr = packed + (e * rows + row) * (k / 2) + s * 32 + (l >> 4) * 4;
       // 4-byte aligned: K / 2 and s * 32 are multiples of 4
       v.x = *reinterpret_cast<const uint32_t*>(wr);
       v.y = *reinterpret_cast<const uint32_t*>(wr + 16);
       const uint8_t* sr = scales + (e * rows + row) * (k / 32) + s * 2;
-      sc = float2{e8m0_scale(sr[0]), e8m0_scale(sr[1])};
+      sb0 = sr[0];
+      sb1 = sr[1];
     }
     pre_b[i] = v;
-    if (l < 16) pre_s[blk * 16 + l] = sc;
+    // the two 16-bit halves, block 2s first (the lower address)
+    if (l < 16) pre_s[blk * 16 + l] = ((sb0 << 7) | 0x40u) | (((sb1 << 7) | 0x40u) << 16);
   }
 }
 
@@ -76,7 +80,7 @@ extern "C" int mxfp4_prepack_w4a16_size(int64_t experts, int64_t rows, int64_t k
 }
 
 extern "C" int mxfp4_prepack_w4a16(const uint8_t* packed, const uint8_t* scales, int64_t experts,
-                                   int64_t rows, int64_t k, uint8_t* pre_b, float* pre_s,
+                                   int64_t rows, int64_t k, uint8_t* pre_b, uint16_t* pre_s,
                                    void* stream) {
   if (experts < 1 || rows < 1 || k <= 0 || k % 64 != 0 || k > 0x7FFFFFFF) {
     set_error("prepack: invalid sizes (experts %lld, rows %lld, k %lld; K must be a multiple "
@@ -94,6 +98,6 @@ extern "C" int mxfp4_prepack_w4a16(const uint8_t* packed, const uint8_t* scales,
   const int64_t blocks = (total + 255) / 256 < 16384 ? (total + 255) / 256 : 16384;
   prepack_w4a16<<<(unsigned)blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
       packed, scales, experts, rows, k, reinterpret_cast<uint2*>(pre_b),
-      reinterpret_cast<float2*>(pre_s));
+      reinterpret_cast<uint32_t*>(pre_s));
   return launch_status("prepack launch");
 }

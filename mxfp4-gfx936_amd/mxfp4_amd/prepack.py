@@ -7,8 +7,8 @@ kernels (aiter:189-205, 229-248; soft:398-399 rejects them).  Here the
 offline repack is explicit: ``prepack_w4a16`` turns (packed, block_scales)
 into a fragment-ordered copy (per 16-row group and 64-deep K step, the
 nibbles in the order the MFMA fragments are read, and the E8M0 bytes as the
-conversion instruction's FP32 scale operands), made once when the weights
-are loaded (the vLLM adapter does it in process_weights_after_loading,
+high halves of the conversion instruction's FP32 scale operands), made once
+when the weights are loaded (the vLLM adapter does it in process_weights_after_loading,
 vllm:68-70).  ``linear_mxfp4_soft(..., prepacked=...)`` and
 ``moe_layer(..., prepacked13=..., prepacked2=...)`` then read the copy in
 their prefill kernels; the results are bitwise equal to the checkpoint-layout
@@ -34,7 +34,7 @@ class PrepackedWeights:
     """Fragment-ordered copy of ``experts`` MXFP4 matrices of ``rows`` x ``k``.
 
     nibbles: uint8 [experts * ceil(rows/16) * k/64 * 512]
-    scales:  float32 [experts * ceil(rows/16) * k/64 * 32]
+    scales:  int16 [experts * ceil(rows/16) * k/64 * 32] (operand high halves)
     """
 
     nibbles: torch.Tensor
@@ -70,7 +70,7 @@ def prepack_w4a16(packed: torch.Tensor, block_scales: torch.Tensor) -> Prepacked
     nb, sb = ctypes.c_int64(), ctypes.c_int64()
     _lib.check(lib.mxfp4_prepack_w4a16_size(experts, rows, k, ctypes.byref(nb), ctypes.byref(sb)))
     nibbles = torch.empty(nb.value, dtype=torch.uint8, device=device)
-    scales = torch.empty(sb.value // 4, dtype=torch.float32, device=device)
+    scales = torch.empty(sb.value // 2, dtype=torch.int16, device=device)
     w = _lib.aligned(p3)
     s = s3.contiguous()
     with _lib.on_device(device):

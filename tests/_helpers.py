@@ -227,11 +227,12 @@ def moe_layer_device(x: torch.Tensor, w13d: torch.Tensor, w2d: torch.Tensor,
 def prepack_layout_np(packed: np.ndarray, scales: np.ndarray):
     """numpy statement of the prepacked weight layout (prepack.hip): for
     [E, rows, K/2] / [E, rows, K/32] uint8 weights, the nibble blocks
-    [E, G, K/64, 64 lanes, 8 bytes] and scale operands [E, G, K/64, 16, 2]
-    as float32 bit patterns (uint32).  Lane l of group g holds the bytes
+    [E, G, K/64, 64 lanes, 8 bytes] and scale operand high halves
+    [E, G, K/64, 16, 2] (uint16).  Lane l of group g holds the bytes
     s*32 + j*16 + (l//16)*4 .. +3 (j = 0, 1) of row g*16 + l%16; scale (r, j)
-    is (byte[2s + j] << 23) | 0x400000 of row g*16 + r; rows past the end are
-    zero nibbles with the operand of byte 127."""
+    is (byte[2s + j] << 7) | 0x40 of row g*16 + r (the float
+    (byte << 23) | 0x400000 without its zero low half); rows past the end
+    are zero nibbles with byte 127."""
     e, rows, half_k = packed.shape
     k = half_k * 2
     g = (rows + 15) // 16
@@ -243,6 +244,6 @@ def prepack_layout_np(packed: np.ndarray, scales: np.ndarray):
     # [e, g, r, s, j, quad, 4 bytes] -> [e, g, s, lane = quad * 16 + r, j, 4]
     pv = p.reshape(e, g, 16, nk, 2, 4, 4).transpose(0, 1, 3, 5, 2, 4, 6)
     nib = pv.reshape(e, g, nk, 64, 8)
-    ops = (s.astype(np.uint32) << 23) | np.uint32(0x400000)
+    ops = ((s.astype(np.uint16) << 7) | np.uint16(0x40)).astype(np.uint16)
     sc = ops.reshape(e, g, 16, nk, 2).transpose(0, 1, 3, 2, 4)
     return np.ascontiguousarray(nib), np.ascontiguousarray(sc)

@@ -29,10 +29,10 @@ def test_prepack_layout_known_positions():
                 assert (got[j * 4:(j + 1) * 4] == packed[ex, 5, off:off + 4]).all()
             assert (nib[ex, 1, st, 37] == 0).all()
             for j in range(2):
-                assert sc[ex, 0, st, 5, j] == (int(scales[ex, 5, 2 * st + j]) << 23) | 0x400000
-                assert sc[ex, 1, st, 5, j] == (127 << 23) | 0x400000
+                assert sc[ex, 0, st, 5, j] == (int(scales[ex, 5, 2 * st + j]) << 7) | 0x40
+                assert sc[ex, 1, st, 5, j] == (127 << 7) | 0x40
             # group 1, row 3 = weight row 19 (live)
-            assert sc[ex, 1, st, 3, 1] == (int(scales[ex, 19, 2 * st + 1]) << 23) | 0x400000
+            assert sc[ex, 1, st, 3, 1] == (int(scales[ex, 19, 2 * st + 1]) << 7) | 0x40
 
 
 def test_prepack_layout_is_a_permutation():
@@ -42,14 +42,16 @@ def test_prepack_layout_is_a_permutation():
     scales = rng.integers(0, 256, size=(3, 48, 8), dtype=np.uint8)
     nib, sc = prepack_layout_np(packed, scales)
     assert np.array_equal(np.sort(nib.reshape(3, -1), axis=1), np.sort(packed.reshape(3, -1), axis=1))
-    # the scale operand's exponent field is the E8M0 byte; mantissa 0x400000
-    assert np.array_equal(np.sort((sc >> 23).reshape(3, -1), axis=1),
+    # the scale operand (the stored half shifted up) has the E8M0 byte as its
+    # exponent field and mantissa 0x400000
+    op = sc.astype(np.uint32) << 16
+    assert np.array_equal(np.sort((op >> 23).reshape(3, -1), axis=1),
                           np.sort(scales.reshape(3, -1).astype(np.uint32), axis=1))
-    assert ((sc & 0x7FFFFF) == 0x400000).all()
-    # the scale operand as a float is 2^(s - 127) for normal bytes ... and the
-    # byte-0 operand 2^-127 (a subnormal float), byte 255 NaN
-    v = sc.view(np.float32)
-    b = (sc >> 23).astype(np.int64)
+    assert ((op & 0x7FFFFF) == 0x400000).all()
+    # the scale operand as a float is 1.5 * 2^(s - 127) for normal bytes,
+    # byte 255 gives NaN
+    v = op.view(np.float32)
+    b = (op >> 23).astype(np.int64)
     normal = (b > 0) & (b < 255)
     assert np.allclose(v[normal], 1.5 * np.exp2(b[normal] - 127.0), rtol=0)
     assert np.isnan(v[b == 255]).all()
