@@ -377,6 +377,29 @@ def test_moe_layer_whole_output(m, layer_weights_full):
     _assert_layer_blocks(y, o32, ref, routes, what=f"moe layer m={m}")
 
 
+@pytest.mark.parametrize("m,top_k", [(2000, 4), (300, 8)])
+def test_moe_layer_skewed_routing_whole_output(m, top_k):
+    # skewed routing over 16 experts (several with no route, some with a
+    # handful): experts padded to half a tile, odd halves run as
+    # half-height tiles, ids int32
+    e, hidden, inter = 16, 512, 256
+    rng = np.random.default_rng(m + top_k)
+    w13, s13 = rand_mxfp4(rng, (e, 2 * inter), hidden)
+    w2, s2 = rand_mxfp4(rng, (e, hidden), inter)
+    pr = np.array([40, 10, 8, 6, 5, 4, 3, 2, 1, 1, 0.5, 0.2, 0.05, 0, 0, 0], dtype=np.float64)
+    ids = np.stack([rng.choice(e, size=top_k, replace=False, p=pr / pr.sum())
+                    for _ in range(m)]).astype(np.int32)
+    w = rng.uniform(0.05, 1.0, size=(m, top_k)).astype(np.float32)
+    x = rand_act(m, (m, hidden))
+    xd, wd, idd = cuda(x), cuda(w), cuda(ids)
+    y = mx.moe_layer(xd, cuda(w13), cuda(s13), cuda(w2), cuda(s2), wd, idd)
+    d13, d2 = _dequant_experts(w13, s13), _dequant_experts(w2, s2)
+    o32, routes = moe_layer_device(xd, d13, d2, wd, idd, "f32", return_routes=True)
+    ref = moe_layer_device(xd, d13, d2, wd, idd, "ref")
+    _assert_layer_blocks(y, o32, ref, routes, what=f"skewed moe layer m={m} top_k={top_k}",
+                         row_block=100)
+
+
 def test_fused_moe_whole_output_m4096(layer_weights_full):
     # the gate_up GEMM of the MoE layer at 4096 tokens (32768 routes over
     # 128-row expert blocks: the persistent routed kernel), every route row
