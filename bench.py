@@ -628,7 +628,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                      "traffic": recorded_traffic(),
-                     "kernel": "w4a16_pf<bf16, prepacked> 128x320 tile, 4 waves of 128x80 "
+                     "kernel": "w4a16_pf<bf16, prepacked> 256x320 tile, 2 x 4 waves of 128x80 "
                                "(direct-to-LDS)",
                      "kernel_us": round(kernel_ms * 1e3, 3),
                      "checkpoint_layout_kernel_us": round(ckpt_ms * 1e3, 3),

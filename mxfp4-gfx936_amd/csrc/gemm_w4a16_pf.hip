@@ -915,6 +915,9 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 template <typename T, int EPI, bool PRE>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
+    case PF_256x320:
+      if constexpr (EPI == EPI_STORE) return launch_cfg<T, 2, 4, 8, 5, 2, EPI, 1, PRE>(g, st);
+      else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // (not chosen)
     case PF_128x320:
       if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // SiLU pairs need even FN
@@ -990,6 +993,15 @@ int pf_choose(const GemmArgs& g, int epi) {
     const int64_t rounds = (t + 511) / 512;
     return t >= 512 ? (double)t / (double)(rounds * 512) : 0.0;
   };
+  // One round of 256 x 320 tiles (8 waves, one workgroup per CU): the CU's
+  // waves finish together instead of a CU's second workgroup running its
+  // epilogue alone at the end (steady clocks, prepacked: qkv M=4096 65.7 ->
+  // 64.6 us, M=4096 K=4096 N=5120 118.8 -> 115.9 us; at two rounds, M=8192,
+  // 125 -> 127 us, so only where the tiles fill 80-100% of one round)
+  if (!routed && epi == EPI_STORE) {
+    const int64_t t = tiles(256, 320), cus = device_cus();
+    if (cus > 0 && t <= cus && t * 5 >= cus * 4) return PF_256x320;
+  }
   if (allowed(128)) {
     const double f256 = fill(256);
     const double f320 = epi == EPI_STORE ? fill(320) : 0.0;
