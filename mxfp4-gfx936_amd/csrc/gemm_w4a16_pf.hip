@@ -918,6 +918,9 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
     case PF_256x320:
       if constexpr (EPI == EPI_STORE) return launch_cfg<T, 2, 4, 8, 5, 2, EPI, 1, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // (not chosen)
+    case PF_256x256:
+      if constexpr (EPI == EPI_STORE) return launch_cfg<T, 2, 4, 8, 4, 2, EPI, 1, PRE>(g, st);
+      else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // (not chosen)
     case PF_128x320:
       if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // SiLU pairs need even FN
@@ -993,14 +996,28 @@ int pf_choose(const GemmArgs& g, int epi) {
     const int64_t rounds = (t + 511) / 512;
     return t >= 512 ? (double)t / (double)(rounds * 512) : 0.0;
   };
-  // One round of 256 x 320 tiles (8 waves, one workgroup per CU): the CU's
-  // waves finish together instead of a CU's second workgroup running its
-  // epilogue alone at the end (steady clocks, prepacked: qkv M=4096 65.7 ->
-  // 64.6 us, M=4096 K=4096 N=5120 118.8 -> 115.9 us; at two rounds, M=8192,
-  // 125 -> 127 us, so only where the tiles fill 80-100% of one round)
+  // One round of 256-row tiles (8 waves of 128 x 80 or 128 x 64, one
+  // workgroup per CU): the CU's waves finish together instead of a CU's
+  // second workgroup running its epilogue alone at the end.  Taken where
+  // the round does >= 90% useful work (M x N over CUs x tile area; steady
+  // clocks, prepacked: qkv M=4096 256 x 320 65.7 -> 64.6 us, M=4096 K=4096
+  // N=5120 118.8 -> 115.9 us, M=K=N=4096 256 x 256 99.2 -> 97.3 us; at 80%,
+  // 256 x 320 on M=K=N=4096 took 107.6 us; two rounds (M=8192) and 8 waves
+  // of 128 x 32 (o_proj M=4096: 58.9 vs 56.2 us) lose)
   if (!routed && epi == EPI_STORE) {
-    const int64_t t = tiles(256, 320), cus = device_cus();
-    if (cus > 0 && t <= cus && t * 5 >= cus * 4) return PF_256x320;
+    const int64_t cus = device_cus();
+    const int cand[2][2] = {{PF_256x320, 320}, {PF_256x256, 256}};
+    int best = -1;
+    double best_eff = 0.9;
+    for (int i = 0; i < 2 && cus > 0; ++i) {
+      if (tiles(256, cand[i][1]) > cus) continue;
+      const double eff = (double)g.m * (double)g.n / ((double)cus * 256.0 * cand[i][1]);
+      if (eff >= best_eff) {
+        best = cand[i][0];
+        best_eff = eff;
+      }
+    }
+    if (best >= 0) return best;
   }
   if (allowed(128)) {
     const double f256 = fill(256);
