@@ -238,6 +238,35 @@ def decode_probe() -> int:
     return 0
 
 
+def moe_probe() -> int:
+    """MoE layer prefill launches for trace runs of the routed GEMMs: E=128,
+    top-8, H=2048, I=768 with prepacked weights, 512 and 4096 tokens, each
+    after an untimed clock ramp, 20 launches."""
+    import numpy as np
+    import torch
+
+    import mxfp4_amd as mx
+    mx._lib.load()
+    e, hidden, inter, top_k = 128, 2048, 768, 8
+    rng = np.random.default_rng(20260815)
+    (w13, s13), = rand_weights(rng, (e, 2 * inter), hidden)
+    (w2, s2), = rand_weights(rng, (e, hidden), inter)
+    pre = {"prepacked13": mx.prepack_w4a16(w13, s13), "prepacked2": mx.prepack_w4a16(w2, s2)}
+    for m in (512, 4096):
+        g = torch.Generator().manual_seed(20260817 + m)
+        w, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
+        w = (w / w.sum(-1, keepdim=True)).cuda()
+        ids = ids.cuda()
+        x = randn_bf16(20260816 + m, (m, hidden))
+        ramp_clocks(lambda: mx.moe_layer(x, w13, s13, w2, s2, w, ids, **pre))
+        for _ in range(20):
+            mx.moe_layer(x, w13, s13, w2, s2, w, ids, **pre)
+        torch.cuda.synchronize()
+        log(f"moe probe m={m} done")
+    print(json.dumps({"probe": "moe", "m": [512, 4096]}))
+    return 0
+
+
 def data_probe() -> int:
     """Steady-clock time of the headline GEMM on random inputs (the bench's)
     and on all-zero / constant ones.  The kernel and the work are the same;
@@ -554,6 +583,8 @@ def main() -> int:
                     help="only run decode launches for counter / trace runs")
     ap.add_argument("--data-probe", action="store_true",
                     help="time the headline GEMM on random vs zero / constant inputs")
+    ap.add_argument("--moe-probe", action="store_true",
+                    help="only run MoE layer prefill launches for trace runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -566,6 +597,8 @@ def main() -> int:
         return decode_probe()
     if args.data_probe:
         return data_probe()
+    if args.moe_probe:
+        return moe_probe()
 
     import numpy as np
     import torch
