@@ -921,6 +921,7 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
     case PF_256x256:
       if constexpr (EPI == EPI_STORE) return launch_cfg<T, 2, 4, 8, 4, 2, EPI, 1, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // (not chosen)
+    case PF_64x256: return launch_cfg<T, 1, 4, 4, 4, 3, EPI, 3, PRE>(g, st);
     case PF_128x320:
       if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // SiLU pairs need even FN
@@ -1026,6 +1027,12 @@ int pf_choose(const GemmArgs& g, int epi) {
     if (f256 >= 0.8) return PF_128x256;
     if (tiles(128, 128) >= 512) return PF_128x128;
   }
+  // Routed 64-row blocks (MoE prefill at ~300-1300 tokens): 64 x 256 tiles,
+  // which stream each expert's weights in half as many tiles (MoE layer,
+  // prepacked, 512 tokens 107.6 -> 105.4 us, 1024 tokens 154.2 -> 144.3 us;
+  // 2 stages lost 35-40%, 4 stages 2-3%; dense mid-M grids lose with it,
+  // having too few tiles)
+  if (routed && allowed(64)) return PF_64x256;
   // 64-row waves halve the decode work per MFMA of 32-row ones; they win
   // from ~200 tiles (qkv K=2048 N=5120, steady clocks: M=370 18.1 -> 16.8
   // us, M=512 23.8 -> 20.7 us; M=256, 160 tiles, stays with 32 rows: 15.6
