@@ -164,6 +164,7 @@ enum PfConfig {
   PF_256x320 = 5,  // 2 x 4 waves of 128 x 80, one per CU (dense, plain store only)
   PF_256x256 = 6,  // 2 x 4 waves of 128 x 64, one per CU (dense, plain store only)
   PF_64x256 = 7,   // 1 x 4 waves of 64 x 64, 3 stages (routed 64-row blocks)
+  PF_32x256 = 8,   // 1 x 4 waves of 32 x 64, 3 stages (routed 32-row blocks)
 };
 bool pf_supported(const GemmArgs& g, int elem_bytes);
 // The prepacked weights of g (pre_b / pre_s) can replace b / bs.

@@ -922,6 +922,7 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
       if constexpr (EPI == EPI_STORE) return launch_cfg<T, 2, 4, 8, 4, 2, EPI, 1, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // (not chosen)
     case PF_64x256: return launch_cfg<T, 1, 4, 4, 4, 3, EPI, 3, PRE>(g, st);
+    case PF_32x256: return launch_cfg<T, 1, 4, 2, 4, 3, EPI, 4, PRE>(g, st);
     case PF_128x320:
       if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // SiLU pairs need even FN
@@ -1033,6 +1034,10 @@ int pf_choose(const GemmArgs& g, int epi) {
   // 2 stages lost 35-40%, 4 stages 2-3%; dense mid-M grids lose with it,
   // having too few tiles)
   if (routed && allowed(64)) return PF_64x256;
+  // and routed 32-row blocks (~30-500 tokens) 32 x 256 (MoE layer,
+  // prepacked, 3 stages: 256 tokens 86.8 -> 81.6 us, 320 tokens 90.5 ->
+  // 83.1 us; 2 stages 84.4 / 86.2 us)
+  if (routed && allowed(32)) return PF_32x256;
   // 64-row waves halve the decode work per MFMA of 32-row ones; they win
   // from ~200 tiles (qkv K=2048 N=5120, steady clocks: M=370 18.1 -> 16.8
   // us, M=512 23.8 -> 20.7 us; M=256, 160 tiles, stays with 32 rows: 15.6

@@ -451,9 +451,11 @@ LayerPlan plan_layer(int64_t m, int top_k, int num_experts, int64_t hidden, int6
   p.routes = m * top_k;
   const double avg = (double)p.routes / (double)num_experts;
   // routing block per average routes per expert (MoE layer, 128 experts,
-  // top-8, steady clocks: 16-row blocks win up to ~10 routes per expert,
-  // 32 up to ~24, 64 up to ~80)
-  p.block_m = avg <= 10.0 ? 16 : (avg <= 24.0 ? 32 : (avg <= 80.0 ? 64 : 128));
+  // top-8, prepacked, steady clocks: 16-row blocks win up to ~1.5 routes per
+  // expert, 32 (32 x 256 tiles) up to ~32, 64 up to ~80; e.g. 96 tokens
+  // 93.6 us with 16 vs 78.4 us with 32, 448 tokens 102.3 us with 64 vs
+  // 96.6 us with 32, 640 tokens 112.3 us with 64 vs 117.3 us with 32)
+  p.block_m = avg <= 1.5 ? 16 : (avg <= 32.0 ? 32 : (avg <= 80.0 ? 64 : 128));
   align_capacity(p.routes, num_experts, p.block_m, &p.max_sorted, &p.max_blocks, &p.nchunks);
   int64_t off = 0;
   p.off_counts = off; off = round_up(off + (p.nchunks > 0 ? p.nchunks : 1) * num_experts * 4, 256);
