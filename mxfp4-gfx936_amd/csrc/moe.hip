@@ -25,9 +25,9 @@ namespace {
 
 constexpr int kChunk = 1024;  // routes per count/place workgroup
 // Routes the single-workgroup routing handles: up to kSingle one 256-thread
-// workgroup (256 routes: 4.9 us); up to kSingleWide one 1024-thread
-// workgroup (1024-route placement chunks; 2048 routes: 6.6 us, 4096: 10.0
-// us, against 15.4 us of kernel time for the three launches).
+// workgroup; up to kSingleWide one 1024-thread workgroup (4096 routes: ~6
+// us in the kernel against 15.4 us of kernel time for the three launches;
+// for up to 1024 routes, 256 threads beat 1024: 5.0 vs 5.4 us).
 constexpr int kSingle = 1024;
 constexpr int kSingleWide = 4096;
 // Layers with at most this many routes use direct routing in the GEMMs
@@ -230,55 +230,81 @@ __global__ __launch_bounds__(256) void topk_sum(const T* __restrict__ d, const T
 }
 
 // All three passes in one workgroup of NT threads for at most NT * RPT
-// routes and kSingleExperts experts (decode and small prefill): the
-// histogram, the padded exclusive scan over experts (each thread owns EPT
-// consecutive experts), and the ballot placement of align_place over chunks
-// of NT routes, separated by barriers instead of launches.  Placement of a
-// chunk: each wave counts its routes per expert (ballots), one pass over
-// the experts turns the counts into each wave's first position (after the
-// earlier chunks and the lower waves), and every route lands at its wave's
-// position + its rank among the lower lanes -- route order within an
-// expert, as align_place.  The counts are double-buffered by chunk parity,
-// so a chunk costs two barriers; chunks past the last route are skipped.
+// routes and kSingleExperts experts (decode and small prefill).  Wave w owns
+// routes w * RPT * 64 .. +RPT * 64 in RPT sub-chunks of 64, so route order
+// is wave, then sub-chunk, then lane.  (1) Each lane finds the lanes of its
+// sub-chunk with the same expert (one ballot per id bit; the masks are kept
+// for step 3) and the lowest of them adds their count to the wave's row of
+// per-expert counts.  (2) One thread per expert sums its wave counts, the
+// padded sizes are scanned over the experts, and the wave rows become each
+// wave's first position per expert; expert ids and sentinel padding are
+// written.  (3) Every route lands at its wave's position for its expert +
+// its rank among the lower lanes, and the lowest lane advances the position
+// for the next sub-chunk -- route order within an expert, as align_place.
+// Three barriers in all (the placement needs none: a wave's LDS accesses
+// are ordered); 4096 routes: 9.1 -> 5.9 us, 1024: 7.7 -> 5.0 us of
+// in-kernel time against per-chunk placement over the whole workgroup.
 template <typename TI, int NT, int RPT>
 __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, int64_t n,
                                                    int num_experts, int id_bits, int block_m,
                                                    int32_t* __restrict__ sorted_ids,
                                                    int32_t* __restrict__ expert_ids,
                                                    int32_t* __restrict__ num_post_padded) {
-  constexpr int W = NT / 64;                              // waves
+  constexpr int W = NT / 64;                // waves
   constexpr int E = kSingleExperts;
-  constexpr int EPT = (E + NT - 1) / NT;                  // experts per thread in the scan
-  __shared__ int cursor[2][E];    // counts, then each expert's next position (by chunk parity)
-  __shared__ int wbase[2][W][E];  // per-wave counts, then per-wave first positions
+  constexpr int EPT = (E + NT - 1) / NT;    // experts per thread in the scan
+  __shared__ int wpos[W][E];                // per-wave counts, then next positions
   __shared__ int part[W];
+  __shared__ int s_fill[E], s_end[E];       // first sentinel slot, end of the padded range
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  for (int i = tid; i < 2 * E; i += NT) (&cursor[0][0])[i] = 0;
-  for (int i = tid; i < 2 * W * E; i += NT) (&wbase[0][0][0])[i] = 0;
-  __syncthreads();
   int eid[RPT];
+  const int64_t rbase = (int64_t)wave * (RPT * 64);
 #pragma unroll
-  for (int it = 0; it < RPT; ++it) {
-    const int64_t r = it * NT + tid;
+  for (int j = 0; j < RPT; ++j) {
+    const int64_t r = rbase + j * 64 + lane;
     int64_t e64 = -1;
     if (r < n) e64 = (int64_t)ids[r];
-    eid[it] = (e64 >= 0 && e64 < num_experts) ? (int)e64 : -1;
+    eid[j] = (e64 >= 0 && e64 < num_experts) ? (int)e64 : -1;
+  }
+  for (int i = tid; i < W * E; i += NT) (&wpos[0][0])[i] = 0;
+  __syncthreads();
+  // (1) lanes of the sub-chunk with the same expert; the RPT ballot chains
+  // are independent, so they are interleaved bit by bit
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint64_t same[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) same[j] = __ballot(eid[j] >= 0);
+  for (int bit = 0; bit < id_bits; ++bit) {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const bool b = (eid[j] >> bit) & 1;  // lanes of invalid ids are out of every mask
+      const uint64_t bal = __ballot(b);
+      same[j] &= b ? bal : ~bal;
+    }
   }
 #pragma unroll
-  for (int it = 0; it < RPT; ++it)
-    if (eid[it] >= 0) atomicAdd(&cursor[0][eid[it]], 1);
+  for (int j = 0; j < RPT; ++j)
+    if (eid[j] >= 0 && __popcll(same[j] & lt_mask) == 0) wpos[wave][eid[j]] += __popcll(same[j]);
   __syncthreads();
-  // padded exclusive scan: thread tid owns experts tid*EPT .. +EPT; the
+  // (2) padded exclusive scan: thread tid owns experts tid*EPT .. +EPT; the
   // per-thread totals are scanned with wave shuffles, then the wave sums
   int cnt[EPT], pad[EPT], local = 0;
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int e = tid * EPT + j;
-    cnt[j] = e < num_experts ? cursor[0][e] : 0;
-    pad[j] = (cnt[j] + block_m - 1) / block_m * block_m;
-    local += pad[j];
+  for (int jj = 0; jj < EPT; ++jj) {
+    const int x = tid * EPT + jj;
+    int c = 0;
+    if (x < num_experts) {
+      int cw[W];  // all reads first: one LDS round trip, not W
+#pragma unroll
+      for (int w = 0; w < W; ++w) cw[w] = wpos[w][x];
+#pragma unroll
+      for (int w = 0; w < W; ++w) c += cw[w];
+    }
+    cnt[jj] = c;
+    pad[jj] = (c + block_m - 1) / block_m * block_m;
+    local += pad[jj];
   }
   int v = local;
 #pragma unroll
@@ -291,49 +317,51 @@ __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, i
   for (int w = 0; w < wave; ++w) v += part[w];
   int start = v - local;
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int e = tid * EPT + j;
-    if (e < num_experts) {
-      cursor[0][e] = start;
-      for (int blk = start / block_m; blk < (start + pad[j]) / block_m; ++blk) expert_ids[blk] = e;
-      for (int p = start + cnt[j]; p < start + pad[j]; ++p) sorted_ids[p] = (int32_t)n;
+  for (int jj = 0; jj < EPT; ++jj) {
+    const int x = tid * EPT + jj;
+    if (x < num_experts) {
+      int p = start;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const int c = wpos[w][x];
+        wpos[w][x] = p;
+        p += c;
+      }
+      for (int blk = start / block_m; blk < (start + pad[jj]) / block_m; ++blk) expert_ids[blk] = x;
+      s_fill[x] = start + cnt[jj];
+      s_end[x] = start + pad[jj];
     }
-    start += pad[j];
+    start += pad[jj];
   }
   if (tid == NT - 1) num_post_padded[0] = v;
   __syncthreads();
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-#pragma unroll
-  for (int it = 0; it < RPT; ++it) {
-    if ((int64_t)it * NT >= n) break;  // the same for every thread
-    const int pb = it & 1;
-    const int64_t r = it * NT + tid;
-    const bool valid = eid[it] >= 0;
-    const int e = valid ? eid[it] : 0;
-    uint64_t same = __ballot(valid);
-    for (int bit = 0; bit < id_bits; ++bit) {
-      const bool b = (e >> bit) & 1;
-      const uint64_t bal = __ballot(b);
-      same &= b ? bal : ~bal;
+  // sentinel padding (at most block_m - 1 slots per expert): consecutive
+  // lanes on consecutive slots of one expert
+  if ((block_m & (block_m - 1)) == 0) {
+    const int sh = __builtin_ctz(block_m);
+    for (int i = tid; i < num_experts * block_m; i += NT) {
+      const int x = i >> sh;
+      const int q = s_fill[x] + (i & (block_m - 1));
+      if (q < s_end[x]) sorted_ids[q] = (int32_t)n;
     }
-    const int rank = __popcll(same & lt_mask);
-    if (valid && rank == 0) wbase[pb][wave][e] = __popcll(same);
-    __syncthreads();
-    for (int x = tid; x < num_experts; x += NT) {
-      int c[W];  // all reads first: one LDS round trip, not W
-#pragma unroll
-      for (int w = 0; w < W; ++w) c[w] = wbase[pb][w][x];
-      int pos = cursor[pb][x];
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        wbase[pb][w][x] = pos;
-        wbase[pb ^ 1][w][x] = 0;  // the next chunk's counts
-        pos += c[w];
-      }
-      cursor[pb ^ 1][x] = pos;
+  } else {
+    for (int i = tid; i < num_experts * block_m; i += NT) {
+      const int x = i / block_m;
+      const int q = s_fill[x] + (i - x * block_m);
+      if (q < s_end[x]) sorted_ids[q] = (int32_t)n;
     }
-    __syncthreads();
-    if (valid) sorted_ids[wbase[pb][wave][e] + rank] = (int32_t)r;
+  }
+  // (3) placement
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    if (rbase + j * 64 >= n) break;  // the same for the whole wave
+    if (eid[j] >= 0) {
+      const int e = eid[j];
+      const int rank = __popcll(same[j] & lt_mask);
+      const int base = wpos[wave][e];
+      sorted_ids[base + rank] = (int32_t)(rbase + j * 64 + lane);
+      if (rank == 0) wpos[wave][e] = base + __popcll(same[j]);
+    }
   }
 }
 

@@ -234,7 +234,10 @@ def test_aiter_entry_pipelined_decode_grid():
 @pytest.mark.parametrize("n_tokens,top_k,num_experts,block_m",
                          [(1, 8, 128, 16), (8, 8, 128, 16), (33, 4, 16, 32), (128, 8, 128, 32),
                           (100, 8, 256, 16), (256, 8, 128, 64), (512, 8, 128, 64),
-                          (700, 3, 7, 128), (64, 4, 300, 16), (4096, 8, 128, 128)])
+                          (700, 3, 7, 128), (64, 4, 300, 16), (4096, 8, 128, 128),
+                          # single-workgroup kernel: a few experts with hundreds of
+                          # routes each, and a block size that is not a power of two
+                          (512, 8, 3, 48), (128, 8, 5, 16), (96, 8, 256, 32)])
 def test_device_routing_matches_oracle(n_tokens, top_k, num_experts, block_m):
     g = torch.Generator().manual_seed(n_tokens * 7 + top_k)
     ids = torch.randint(-1, num_experts + 1, (n_tokens, top_k), generator=g)
