@@ -187,6 +187,153 @@ __global__ __launch_bounds__(256) void align_place(const TI* __restrict__ ids, i
   }
 }
 
+// Scan and placement in one launch, after align_count, for at most
+// kScanPlaceChunks chunks: workgroup c places chunk c's kChunk routes and
+// first derives what it needs from the per-chunk counts itself -- for each
+// expert the routes of the earlier chunks and of all chunks (coalesced
+// loads, summed with LDS atomics), the padded exclusive scan over the
+// experts -- instead of waiting for a separate scan launch (redundant work
+// of nchunks x E count loads per workgroup, all L2 hits).  Placement as in
+// align_single: wave w owns routes w * RPT * 64 .. +RPT * 64 of the chunk,
+// the lanes of a sub-chunk with the same expert come from ballots, per-wave
+// counts become per-wave positions, and each wave then places its
+// sub-chunks in order without barriers.  Workgroup c also writes, by whole
+// waves, expert_ids and the sentinel padding of the experts x with x %
+// nchunks == c, and workgroup 0 the padded route count.
+constexpr int kScanPlaceChunks = 64;
+
+template <typename TI>
+__global__ __launch_bounds__(512) void align_scan_place(const TI* __restrict__ ids, int64_t n,
+                                                        int num_experts, int id_bits, int block_m,
+                                                        const int32_t* __restrict__ counts,
+                                                        int nchunks,
+                                                        int32_t* __restrict__ sorted_ids,
+                                                        int32_t* __restrict__ expert_ids,
+                                                        int32_t* __restrict__ num_post_padded) {
+  constexpr int NT = 512, W = NT / 64, RPT = kChunk / NT;
+  constexpr int EPT = kMaxExperts / NT;  // experts per thread in the scan
+  constexpr int CB = 16;                 // count loads per thread per round trip
+  __shared__ int wpos[W * kMaxExperts];  // [wave][expert]: counts, then next positions
+  __shared__ int s_pre[kMaxExperts], s_tot[kMaxExperts];  // then fill start / padded end
+  __shared__ int part[W];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c = (int)blockIdx.x;
+  const int ne = num_experts;
+  int eid[RPT];
+  const int64_t rbase = (int64_t)c * kChunk + (int64_t)wave * (RPT * 64);
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int64_t r = rbase + j * 64 + lane;
+    int64_t e64 = -1;
+    if (r < n) e64 = (int64_t)ids[r];
+    eid[j] = (e64 >= 0 && e64 < ne) ? (int)e64 : -1;
+  }
+  const int ncnt = nchunks * ne;
+  int cv[CB];
+#pragma unroll
+  for (int b = 0; b < CB; ++b) cv[b] = tid + b * NT < ncnt ? counts[tid + b * NT] : 0;
+  for (int i = tid; i < W * ne; i += NT) wpos[i] = 0;
+  for (int x = tid; x < ne; x += NT) s_pre[x] = s_tot[x] = 0;
+  __syncthreads();
+  // counts[cc][x] -> routes of expert x in all chunks and in chunks < c
+  // (i / ne by a float reciprocal and one correction: i < 2^16)
+  const float inv_ne = 1.0f / (float)ne;
+  for (int i0 = 0; i0 < ncnt; i0 += CB * NT) {
+    if (i0 > 0) {
+#pragma unroll
+      for (int b = 0; b < CB; ++b)
+        cv[b] = i0 + tid + b * NT < ncnt ? counts[i0 + tid + b * NT] : 0;
+    }
+#pragma unroll
+    for (int b = 0; b < CB; ++b) {
+      const int i = i0 + tid + b * NT;
+      if (i < ncnt && cv[b] != 0) {
+        int cc = (int)((float)i * inv_ne);
+        cc += (cc + 1) * ne <= i ? 1 : 0;
+        cc -= cc * ne > i ? 1 : 0;
+        const int x = i - cc * ne;
+        atomicAdd(&s_tot[x], cv[b]);
+        if (cc < c) atomicAdd(&s_pre[x], cv[b]);
+      }
+    }
+  }
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint64_t same[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) same[j] = __ballot(eid[j] >= 0);
+  for (int bit = 0; bit < id_bits; ++bit) {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const bool b = (eid[j] >> bit) & 1;  // lanes of invalid ids are out of every mask
+      const uint64_t bal = __ballot(b);
+      same[j] &= b ? bal : ~bal;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < RPT; ++j)
+    if (eid[j] >= 0 && __popcll(same[j] & lt_mask) == 0)
+      wpos[wave * ne + eid[j]] += __popcll(same[j]);
+  __syncthreads();
+  // padded exclusive scan over the experts (thread-local EPT, wave
+  // shuffles, then the wave sums)
+  int tot[EPT], pad[EPT], local = 0;
+#pragma unroll
+  for (int jj = 0; jj < EPT; ++jj) {
+    const int x = tid * EPT + jj;
+    tot[jj] = x < ne ? s_tot[x] : 0;
+    pad[jj] = (tot[jj] + block_m - 1) / block_m * block_m;
+    local += pad[jj];
+  }
+  int v = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off);
+    if (lane >= off) v += u;
+  }
+  if (lane == 63) part[wave] = v;
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) v += part[w];
+  int start = v - local;
+#pragma unroll
+  for (int jj = 0; jj < EPT; ++jj) {
+    const int x = tid * EPT + jj;
+    if (x < ne) {
+      int p = start + s_pre[x];
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const int cw = wpos[w * ne + x];
+        wpos[w * ne + x] = p;
+        p += cw;
+      }
+      s_pre[x] = start;           // now: first slot of the expert
+      s_tot[x] = start + tot[jj];  // now: first sentinel slot
+    }
+    start += pad[jj];
+  }
+  if (c == 0 && tid == NT - 1) num_post_padded[0] = v;
+  __syncthreads();
+  // expert ids and sentinel padding of this workgroup's experts, by waves
+  for (int x = c + wave * nchunks; x < ne; x += W * nchunks) {
+    const int st = s_pre[x], fill = s_tot[x];
+    const int end = fill == st ? st : st + (fill - st + block_m - 1) / block_m * block_m;
+    for (int i = lane; i < (end - st) / block_m; i += 64) expert_ids[st / block_m + i] = x;
+    for (int q = fill + lane; q < end; q += 64) sorted_ids[q] = (int32_t)n;
+  }
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    if (rbase + j * 64 >= n) break;  // the same for the whole wave
+    if (eid[j] >= 0) {
+      const int e = eid[j];
+      const int rank = __popcll(same[j] & lt_mask);
+      const int base = wpos[wave * ne + e];
+      sorted_ids[base + rank] = (int32_t)(rbase + j * 64 + lane);
+      if (rank == 0) wpos[wave * ne + e] = base + __popcll(same[j]);
+    }
+  }
+}
+
 // out[t, :] = sum over slots s of d[t * top_k + s, :] (FP32, slot order),
 // skipping slots whose expert id is outside [0, E) (their rows are zero in
 // the reference, soft:476).  vllm:263-265.
@@ -411,6 +558,12 @@ int launch_align(const TI* ids, int64_t n, int num_experts, int block_m, int32_t
     align_count<TI><<<(unsigned)nchunks, 256, 0, st>>>(ids, n, num_experts, counts);
     int rc = launch_status("align count launch");
     if (rc) return rc;
+  }
+  if (nchunks > 0 && nchunks <= kScanPlaceChunks) {
+    align_scan_place<TI><<<(unsigned)nchunks, 512, 0, st>>>(ids, n, num_experts, id_bits, block_m,
+                                                             counts, (int)nchunks, sorted_ids,
+                                                             expert_ids, npp);
+    return launch_status("align scan+place launch");
   }
   align_scan<<<1, kMaxExperts, 0, st>>>(counts, (int)nchunks, num_experts, block_m, n, sorted_ids,
                                         expert_ids, npp);

@@ -237,7 +237,11 @@ def test_aiter_entry_pipelined_decode_grid():
                           (700, 3, 7, 128), (64, 4, 300, 16), (4096, 8, 128, 128),
                           # single-workgroup kernel: a few experts with hundreds of
                           # routes each, and a block size that is not a power of two
-                          (512, 8, 3, 48), (128, 8, 5, 16), (96, 8, 256, 32)])
+                          (512, 8, 3, 48), (128, 8, 5, 16), (96, 8, 256, 32),
+                          # per-chunk counts + one scan-and-place launch (<= 64
+                          # chunks of 1024 routes), and the three-launch path beyond
+                          (2048, 8, 512, 32), (600, 8, 1024, 16), (8192, 8, 128, 64),
+                          (513, 8, 256, 16), (9000, 8, 64, 128)])
 def test_device_routing_matches_oracle(n_tokens, top_k, num_experts, block_m):
     g = torch.Generator().manual_seed(n_tokens * 7 + top_k)
     ids = torch.randint(-1, num_experts + 1, (n_tokens, top_k), generator=g)
