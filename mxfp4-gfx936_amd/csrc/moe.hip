@@ -632,11 +632,16 @@ LayerPlan plan_layer(int64_t m, int top_k, int num_experts, int64_t hidden, int6
   p.routes = m * top_k;
   const double avg = (double)p.routes / (double)num_experts;
   // routing block per average routes per expert (MoE layer, 128 experts,
-  // top-8, prepacked, steady clocks: 16-row blocks win up to ~1.5 routes per
-  // expert, 32 (32 x 256 tiles) up to ~32, 64 up to ~80; e.g. 96 tokens
-  // 93.6 us with 16 vs 78.4 us with 32, 448 tokens 102.3 us with 64 vs
-  // 96.6 us with 32, 640 tokens 112.3 us with 64 vs 117.3 us with 32)
-  p.block_m = avg <= 1.5 ? 16 : (avg <= 32.0 ? 32 : (avg <= 80.0 ? 64 : 128));
+  // top-8, prepacked, steady clocks): 16-row blocks up to ~1.5 routes per
+  // expert, 32 (32 x 256 tiles) up to ~32, 64 (64 x 256 tiles) above.
+  // E.g. 96 tokens 93.6 us with 16 vs 78.4 us with 32; 448 tokens 102.3 us
+  // with 64 vs 96.6 us with 32; 640 tokens 112.3 us with 64 vs 117.3 us
+  // with 32.  Against 128-row blocks (persistent 128 x 256 tiles, whose
+  // fixed rounds of 512 workgroups quantize): 2048 tokens 236 -> 224 us,
+  // 4096 385 -> 372 us, 6144 559 -> 521 us, 16384 1289 -> 1283 us; 128 rows
+  // win only where their tiles just fill whole rounds (1536 tokens 166 vs
+  // 182 us, 1664 170 vs 184 us).
+  p.block_m = avg <= 1.5 ? 16 : (avg <= 32.0 ? 32 : 64);
   align_capacity(p.routes, num_experts, p.block_m, &p.max_sorted, &p.max_blocks, &p.nchunks);
   int64_t off = 0;
   p.off_counts = off; off = round_up(off + (p.nchunks > 0 ? p.nchunks : 1) * num_experts * 4, 256);

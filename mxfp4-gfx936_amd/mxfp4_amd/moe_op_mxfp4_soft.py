@@ -78,15 +78,13 @@ def _is_validated_triton_linear_shape(m: int, n: int) -> bool:
 def _routing_block_m(num_routes: int, num_experts: int) -> int:
     """Rows per expert block for the routed GEMMs, from the mean rows per
     expert (the MoE layer's rule: 32-row blocks run 32 x 256 tiles and win
-    from ~1.5 rows per expert, 64-row ones from ~32)."""
+    from ~1.5 rows per expert, 64-row ones, on 64 x 256 tiles, from ~32)."""
     avg = num_routes / max(num_experts, 1)
     if avg <= 1.5:
         return 16
     if avg <= 32:
         return 32
-    if avg <= 80:
-        return 64
-    return 128
+    return 64
 
 
 def dequant_mxfp4(
