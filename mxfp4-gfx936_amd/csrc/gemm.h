@@ -165,6 +165,8 @@ enum PfConfig {
   PF_256x256 = 6,  // 2 x 4 waves of 128 x 64, one per CU (dense, plain store only)
   PF_64x256 = 7,   // 1 x 4 waves of 64 x 64, 3 stages (routed 64-row blocks)
   PF_32x256 = 8,   // 1 x 4 waves of 32 x 64, 3 stages (routed 32-row blocks)
+  PF_32x384 = 9,   // 1 x 4 waves of 32 x 96, 2 stages (routed 32-row blocks, SiLU)
+  PF_32x512 = 10,  // 1 x 4 waves of 32 x 128, 2 stages (routed 32-row blocks)
 };
 bool pf_supported(const GemmArgs& g, int elem_bytes);
 // The prepacked weights of g (pre_b / pre_s) can replace b / bs.

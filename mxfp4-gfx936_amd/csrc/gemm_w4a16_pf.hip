@@ -923,6 +923,8 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // (not chosen)
     case PF_64x256: return launch_cfg<T, 1, 4, 4, 4, 3, EPI, 3, PRE>(g, st);
     case PF_32x256: return launch_cfg<T, 1, 4, 2, 4, 3, EPI, 4, PRE>(g, st);
+    case PF_32x384: return launch_cfg<T, 1, 4, 2, 6, 2, EPI, 4, PRE>(g, st);
+    case PF_32x512: return launch_cfg<T, 1, 4, 2, 8, 2, EPI, 3, PRE>(g, st);
     case PF_128x320:
       if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // SiLU pairs need even FN
@@ -1036,8 +1038,22 @@ int pf_choose(const GemmArgs& g, int epi) {
   if (routed && allowed(64)) return PF_64x256;
   // and routed 32-row blocks (~30-500 tokens) 32 x 256 (MoE layer,
   // prepacked, 3 stages: 256 tokens 86.8 -> 81.6 us, 320 tokens 90.5 ->
-  // 83.1 us; 2 stages 84.4 / 86.2 us)
-  if (routed && allowed(32)) return PF_32x256;
+  // 83.1 us; 2 stages 84.4 / 86.2 us) -- unless that grid would spill past
+  // one round of the 4 resident workgroups per CU: then wider 2-stage tiles
+  // that fit in one (32 x 384 for the SiLU GEMM, 4 per CU; 32 x 512 for
+  // the plain one, 3 per CU).  Expected live blocks: routes / 32 plus half
+  // a block per busy expert.  MoE layer, graph replays over 3 weight copies:
+  // 512 tokens 106.8 -> 99.4 us, 448 tokens 99.7 -> 98.5 us; the wider
+  // tiles lose 2-3 us where 32 x 256 fits in one round (96-384 tokens).
+  if (routed && allowed(32)) {
+    const int64_t cus = device_cus();
+    const int64_t busy = g.num_experts < g.num_valid ? g.num_experts : g.num_valid;
+    const int64_t blocks = g.num_valid / 32 + busy / 2;
+    const int out_cols = epi == EPI_SILU_MUL ? 128 : 256;
+    const int64_t t256 = blocks * ((g.n + out_cols - 1) / out_cols);
+    if (cus > 0 && t256 > 4 * cus) return epi == EPI_SILU_MUL ? PF_32x384 : PF_32x512;
+    return PF_32x256;
+  }
   // 64-row waves halve the decode work per MFMA of 32-row ones; they win
   // from ~200 tiles (qkv K=2048 N=5120, steady clocks: M=370 18.1 -> 16.8
   // us, M=512 23.8 -> 20.7 us; M=256, 160 tiles, stays with 32 rows: 15.6
