@@ -167,6 +167,7 @@ enum PfConfig {
   PF_32x256 = 8,   // 1 x 4 waves of 32 x 64, 3 stages (routed 32-row blocks)
   PF_32x384 = 9,   // 1 x 4 waves of 32 x 96, 2 stages (routed 32-row blocks, SiLU)
   PF_32x512 = 10,  // 1 x 4 waves of 32 x 128, 2 stages (routed 32-row blocks)
+  PF_64x384 = 11,  // 1 x 4 waves of 64 x 96, 2 stages (routed 64-row blocks, SiLU)
 };
 bool pf_supported(const GemmArgs& g, int elem_bytes);
 // The prepacked weights of g (pre_b / pre_s) can replace b / bs.

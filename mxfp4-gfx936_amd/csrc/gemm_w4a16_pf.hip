@@ -925,6 +925,7 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
     case PF_32x256: return launch_cfg<T, 1, 4, 2, 4, 3, EPI, 4, PRE>(g, st);
     case PF_32x384: return launch_cfg<T, 1, 4, 2, 6, 2, EPI, 4, PRE>(g, st);
     case PF_32x512: return launch_cfg<T, 1, 4, 2, 8, 2, EPI, 3, PRE>(g, st);
+    case PF_64x384: return launch_cfg<T, 1, 4, 4, 6, 2, EPI, 3, PRE>(g, st);
     case PF_128x320:
       if constexpr (EPI != EPI_SILU_MUL) return launch_cfg<T, 1, 4, 8, 5, 2, EPI, 2, PRE>(g, st);
       else return launch_cfg<T, 1, 4, 8, 4, 2, EPI, 2, PRE>(g, st);  // SiLU pairs need even FN
@@ -1035,7 +1036,13 @@ int pf_choose(const GemmArgs& g, int epi) {
   // prepacked, 512 tokens 107.6 -> 105.4 us, 1024 tokens 154.2 -> 144.3 us;
   // 2 stages lost 35-40%, 4 stages 2-3%; dense mid-M grids lose with it,
   // having too few tiles)
-  if (routed && allowed(64)) return PF_64x256;
+  // The SiLU GEMM of 64-row blocks takes 64 x 384 tiles of 2 stages (192
+  // outputs; two thirds of the tiles, each of its activation rows read by
+  // 4 column tiles instead of 6): 1024 tokens 135.4 -> 129.8 us, 2048
+  // 206.4 -> 199.2, 4096 354.6 -> 347.0, 8192 646 -> 627 us; neutral at
+  // 640-1280.  (For the plain GEMM, 64 x 384 / 64 x 512 were 3-10 us
+  // slower at 768-1024 tokens and ~2% faster elsewhere: not taken.)
+  if (routed && allowed(64)) return epi == EPI_SILU_MUL ? PF_64x384 : PF_64x256;
   // and routed 32-row blocks (~30-500 tokens) 32 x 256 (MoE layer,
   // prepacked, 3 stages: 256 tokens 86.8 -> 81.6 us, 320 tokens 90.5 ->
   // 83.1 us; 2 stages 84.4 / 86.2 us) -- unless that grid would spill past
