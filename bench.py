@@ -306,6 +306,46 @@ def data_probe() -> int:
     return 0
 
 
+PROBE_LIB = os.path.join(ROOT, "mxfp4-gfx936_amd", "mxfp4_amd", "libmxfp4_probe.so")
+_floor_cache = {}
+
+
+def read_floor_us(torch, nbytes):
+    """Device time (us) of one launch of a plain HBM read of `nbytes`
+    (csrc/probe/read_floor.hip: every load in flight before any is used),
+    graph-replayed over rotating buffers of >= 600 MB in all, as the decode
+    rows are: the floor a single decode launch over those bytes cannot beat.
+    None when the probe library is not built."""
+    import ctypes
+    nbytes = (int(nbytes) + 15) // 16 * 16
+    if nbytes in _floor_cache:
+        return _floor_cache[nbytes]
+    if not os.path.exists(PROBE_LIB):
+        return None
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.mxfp4_probe_read_floor_sink_words.restype = ctypes.c_int64
+    lib.mxfp4_probe_read_floor_sink_words.argtypes = [ctypes.c_int64]
+    lib.mxfp4_probe_read_floor.restype = ctypes.c_int
+    lib.mxfp4_probe_read_floor.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_void_p]
+    copies = max(1, min(128, (600 << 20) // nbytes))
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 256)
+            for _ in range(copies)]
+    words = int(lib.mxfp4_probe_read_floor_sink_words(nbytes))
+    sink = torch.empty(words, dtype=torch.int32, device="cuda")
+
+    def fn(b):
+        rc = lib.mxfp4_probe_read_floor(b.data_ptr(), nbytes, sink.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError("read-floor probe launch failed")
+
+    t = time_graph([lambda b=b: fn(b) for b in bufs], replays=10) * 1e3
+    del bufs, sink
+    _floor_cache[nbytes] = t
+    return t
+
+
 def linear_bytes(m, n, k, prepacked=False):
     """Algorithmic bytes of one W4A16 linear: weights (nibbles + scales: one
     byte per 32 on the checkpoint layout, two in the prepacked copy), x, out."""
@@ -339,8 +379,14 @@ def sweep(mx, torch, np):
                 "TFLOP/s": round(fl / t / 1e9, 2),
                 "mfma_frac": round(fl / t / 1e9 / BF16_PEAK_TFLOPS, 4),
                 "weight_copies": copies}
-            log(f"{name} m={m}: {res[f'w4a16_{name}_m{m}']}")
             del ws, pres
+            if m <= 8:
+                fl_us = read_floor_us(torch, b)
+                if fl_us is not None:
+                    res[f"w4a16_{name}_m{m}"].update(
+                        {"read_floor_us": round(fl_us, 3),
+                         "floor_frac": round(fl_us / (t * 1e3), 4)})
+            log(f"{name} m={m}: {res[f'w4a16_{name}_m{m}']}")
     torch.cuda.empty_cache()
     # --- routed MoE layer (BASELINE configs 3 and 5)
     e, hidden, inter, top_k = 128, 2048, 768, 8
@@ -373,6 +419,11 @@ def sweep(mx, torch, np):
             "us": round(t * 1e3, 2), "e_active": e_active, "GB/s": round(b / t / 1e6, 1),
             "hbm_frac": round(b / t / 1e6 / HBM_PEAK_GBS, 4), "TFLOP/s": round(fl / t / 1e9, 2),
             "mfma_frac": round(fl / t / 1e9 / BF16_PEAK_TFLOPS, 4)}
+        if m <= 32:
+            fl_us = read_floor_us(torch, b)
+            if fl_us is not None:
+                res[f"moe_layer_m{m}"].update({"read_floor_us": round(fl_us, 3),
+                                               "floor_frac": round(fl_us / (t * 1e3), 4)})
         log(f"moe m={m}: {res[f'moe_layer_m{m}']}")
     del layer_copies
     torch.cuda.empty_cache()

@@ -2,7 +2,9 @@
 
 ``python mxfp4-gfx936_amd/build.py`` compiles every ``csrc/*.hip`` with
 hipcc (in parallel, objects under ``_build/``) and links
-``mxfp4_amd/libmxfp4_gfx950.so`` next to the Python package that loads it.
+``mxfp4_amd/libmxfp4_gfx950.so`` next to the Python package that loads it,
+and ``mxfp4_amd/libmxfp4_probe.so`` (``csrc/probe/``: a plain HBM read that
+bench.py times as the floor of the decode kernels; not part of the library).
 
 Flags: ``-O3`` for gfx950 only; packed-FP32 instruction selection is turned
 off (``-Xclang -target-feature -Xclang -packed-fp32-ops``); denormals are
@@ -23,6 +25,9 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "mxfp4_amd", "libmxfp4_gfx950.so")
+# measurement aid for bench.py (a plain HBM read), kept out of the library
+PROBE_SRC = os.path.join(CSRC, "probe", "read_floor.hip")
+PROBE_LIB = os.path.join(HERE, "mxfp4_amd", "libmxfp4_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -69,6 +74,14 @@ def build(verbose: bool = False) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [HIPCC, *CFLAGS, "-shared", PROBE_SRC, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC}:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
     return LIB
 
 
