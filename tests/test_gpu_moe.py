@@ -381,9 +381,9 @@ def test_moe_layer_fp16_and_invalid_ids():
 
 
 def test_moe_layer_fp16_multi_round_grid():
-    # fp16 layer with ~90 routed 128-row blocks: both GEMMs have more tiles
-    # than resident workgroups (the persistent kernel, SiLU and plain
-    # epilogues); sampled rows against the fp16-rounded oracle
+    # fp16 layer with ~165 routed 64-row blocks: both GEMMs have more tiles
+    # than resident workgroups (64 x 384 SiLU tiles, 64 x 256 plain ones);
+    # sampled rows against the fp16-rounded oracle
     rng = np.random.default_rng(2600)
     e, hidden, inter, top_k, m = 8, 2048, 768, 4, 2600
     w13, s13 = rand_mxfp4(rng, (e, 2 * inter), hidden, lo=116, hi=121)
@@ -402,6 +402,27 @@ def test_moe_layer_fp16_multi_round_grid():
                         routes=routes, fmt="f16")
 
 
+def test_moe_layer_fp16_wide_routed_tiles():
+    # fp16 layer at 480 tokens over 128 experts: 32-row blocks whose 32 x 256
+    # grids would spill past one round, so the SiLU GEMM runs 32 x 384 and
+    # the plain one 32 x 512 tiles (2 stages); sampled rows against the
+    # fp16-rounded oracle
+    rng = np.random.default_rng(480)
+    e, hidden, inter, top_k, m = 128, 2048, 768, 8, 480
+    w13, s13 = rand_mxfp4(rng, (e, 2 * inter), hidden, lo=116, hi=121)
+    w2, s2 = rand_mxfp4(rng, (e, hidden), inter, lo=116, hi=121)
+    x = rand_act(481, (m, hidden), torch.float16)
+    w, ids = _route(m, e, top_k, 482)
+    y = mx.moe_layer(cuda(x), cuda(w13), cuda(s13), cuda(w2), cuda(s2), cuda(w), cuda(ids))
+    rows = np.sort(np.random.default_rng(483).choice(m, 40, False))
+    oracle, routes = _fp16_layer_oracle(x.float().numpy()[rows], w13, s13, w2, s2,
+                                        w.numpy()[rows], ids.numpy()[rows])
+    t = torch.from_numpy
+    safe = O.moe_layer_safe(x[rows], t(w13), t(s13), t(w2), t(s2), w[rows], ids[rows])
+    assert_layer_parity(y[t(rows).cuda()], oracle, safe, what="fp16 layer, wide routed tiles",
+                        routes=routes, fmt="f16")
+
+
 @pytest.mark.parametrize("m,n,k,dtype,block_m",
                          [(2300, 3072, 256, torch.float16, 128),
                           (2048, 2048, 256, torch.bfloat16, 128),
@@ -410,7 +431,7 @@ def test_moe_layer_fp16_multi_round_grid():
 def test_routed_gemm_multi_round_grid(m, n, k, dtype, block_m):
     # several rounds of tiles: 68-75 routed 128-row blocks (the persistent
     # kernel; 128 x 256 tiles at N = 3072, whose rounds are 88% full,
-    # 128 x 128 at N = 2048), or 83-108 blocks of 64 rows (64 x 128 tiles,
+    # 128 x 128 at N = 2048), or 83-108 blocks of 64 rows (64 x 256 tiles,
     # 3 stages).  Expert -1 blocks, ids outside [0, E) (rows left
     # untouched), route weights, per-expert scales
     rng = np.random.default_rng(n + k)
