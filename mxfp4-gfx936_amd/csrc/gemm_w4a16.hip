@@ -411,7 +411,8 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
 // epilogues.  Same loads, rounding and reduction order as the skinny
 // kernel, so results are identical.
 template <typename T, int WK, int WN, int U, int CS, int EPI>
-__global__ __launch_bounds__(WK * WN * 64) void w4a16_stream(GemmArgs g) {
+__global__ __launch_bounds__(WK * WN * 64) __attribute__((amdgpu_waves_per_eu(CS >= 4 ? 3 : 1)))
+void w4a16_stream(GemmArgs g) {
   typedef typename V8Of<T>::type V8;
   constexpr int NB = (EPI == EPI_SILU_MUL) ? 2 : 1;
   static_assert(U == 2 || U == 4, "scale loads cover 2 or 4 units");
@@ -861,8 +862,10 @@ void stream_launch_cs(const GemmArgs& g, const SkinnyShape& s, dim3 grid, hipStr
 // 47.4 -> 43.1 us and M=32 97.0 -> 87.5 us with 2 steps; 4 steps (167-172
 // VGPRs, two waves per SIMD) 45.5 / 88.5 us; at M=1 (8 expert blocks) both
 // lose to the skinny kernel.
-int stream_steps(const GemmArgs& g, const SkinnyShape& s, int64_t blocks, int64_t groups) {
+int stream_steps(const GemmArgs& g, const SkinnyShape& s, int64_t blocks, int64_t groups,
+                 int epi) {
   if (s.rb != 1 || s.cg != 1 || (g.k + 127) / 128 > s.wk * s.u) return 1;
+  if (epi == EPI_SILU_MUL && blocks * ((groups + 3) / 4) >= 512) return 4;
   return blocks * ((groups + 1) / 2) >= 512 ? 2 : 1;
 }
 
@@ -943,10 +946,11 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
     SkinnyShape sh1 = sh;
     sh1.cg = 1;
     const int64_t groups1 = (out_cols + 16 * sh1.wn - 1) / (16 * sh1.wn);
-    const int cs = stream_steps(g, sh1, blocks, groups1);
+    const int cs = stream_steps(g, sh1, blocks, groups1, EPI);
     if (cs > 1) {
       dim3 grid((unsigned)((groups1 + cs - 1) / cs), (unsigned)(gy > 0 ? gy : 1));
-      stream_launch_cs<T, 2, EPI>(g, sh1, grid, st);
+      if (cs == 4) stream_launch_cs<T, 4, EPI>(g, sh1, grid, st);
+      else stream_launch_cs<T, 2, EPI>(g, sh1, grid, st);
       return launch_status("w4a16 stream launch");
     }
     const int tile_cols = 16 * sh.wn * sh.cg;
