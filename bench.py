@@ -441,13 +441,19 @@ def sweep(mx, torch, np):
     for cdt, name, peak in ((torch.float32, "f32", FP32_PEAK_TFLOPS),
                             (torch.bfloat16, "bf16", BF16_PEAK_TFLOPS)):
         C = torch.empty((m, top_k, n), dtype=cdt, device="cuda")
-        t = time_eager(lambda: mx.fused_moe_mxfp4_soft(a, wp, C, one, ones_e, None, wsc, tw, ids,
-                                                       empty, empty, empty, True, top_k, False,
-                                                       False), 20, 3)[1]
+
+        def call():
+            mx.fused_moe_mxfp4_soft(a, wp, C, one, ones_e, None, wsc, tw, ids, empty, empty,
+                                    empty, True, top_k, False, False)
+        # device time from graph replays (the op never synchronises the
+        # host); eager_us adds the Python validation and launch overhead
+        t = time_graph([call] * 4, replays=10)
+        te = time_eager(call, 20, 3)[1]
         fl = 2.0 * m * top_k * n * k
         res[f"fused_moe_soft_c{name}_m{m}"] = {
             "us": round(t * 1e3, 2), "TFLOP/s": round(fl / t / 1e9, 2),
-            "peak_frac": round(fl / t / 1e9 / peak, 4), "peak": peak}
+            "peak_frac": round(fl / t / 1e9 / peak, 4), "peak": peak,
+            "eager_us": round(te * 1e3, 2)}
         log(f"fused moe soft C {name}: {res[f'fused_moe_soft_c{name}_m{m}']}")
     del wp, wsc
     # --- W4A4, activations/weights quantized with the RNE rule
