@@ -516,15 +516,17 @@ def test_route_topk_feeds_the_layer(layer_weights):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m,top_k,hidden,inter", [(4, 16, 2048, 768), (3, 6, 1024, 256)],
-                         ids=["k16_two_k_waves", "k6_masked_routes"])
-def test_moe_layer_fused_decode_top_k(m, top_k, hidden, inter, dtype):
+@pytest.mark.parametrize("m,top_k,hidden,inter,e",
+                         [(4, 16, 2048, 768, 32), (3, 6, 1024, 256, 32), (8, 8, 2048, 768, 128)],
+                         ids=["k16_two_k_waves", "k6_masked_routes", "k8_four_column_steps"])
+def test_moe_layer_fused_decode_top_k(m, top_k, hidden, inter, e, dtype):
     # the fused down + top-k kernel (<= 64 routes): top_k 16 fills four
     # route waves and, at 512 workgroups of 16 waves, takes two K waves of
     # up to two trips; top_k 6 leaves two of a wave's four route slots
-    # empty and takes 8-column workgroups (192 workgroups)
+    # empty and takes 8-column workgroups (192 workgroups).  8 tokens over
+    # 128 experts: the gate_up stream kernel takes four column steps per
+    # workgroup (64 row blocks x 12 workgroups)
     rng = np.random.default_rng(600 + top_k)
-    e = 32
     # small scales keep every fp16 intermediate finite
     w13, s13 = rand_mxfp4(rng, (e, 2 * inter), hidden, lo=116, hi=121)
     w2, s2 = rand_mxfp4(rng, (e, hidden), inter, lo=116, hi=121)
