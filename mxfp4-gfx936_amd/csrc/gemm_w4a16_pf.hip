@@ -911,7 +911,12 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
 // (the extra LDS costs a workgroup per CU: -10-20% for the routed GEMMs);
 // 4-8 stages at 32 x 128 and 5 at 64 x 128 (M = 256-1024: 0-15% slower);
 // weights prefetched 2-4 stages ahead of the activations (no gain: the
-// routed GEMMs wait on activation rows as much).
+// routed GEMMs wait on activation rows as much); two K-groups of 4 waves
+// per 64 x 128 tile, each computing alternate 64-deep halves of 128-deep
+// stages, partial sums added through LDS (8 waves for grids of ~1 tile per
+// CU): qkv M = 370 / 512 / 768 only 2 / 4 / 5% faster, 32 x 128 and split-K
+// shapes slower, and the summation order would differ between the
+// prepacked and checkpoint layouts.
 template <typename T, int EPI, bool PRE>
 int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   switch (cfg) {
