@@ -308,6 +308,53 @@ def test_vllm_adapter_moe_and_dense_on_device(layer_weights):
     assert torch.equal(yd, mx.linear_mxfp4_soft(x, cuda(w13[0]), cuda(s13[0])))
 
 
+def test_vllm_reference_debug_path_on_device(layer_weights, monkeypatch):
+    # MXFP4_IMPLEMENTATION=reference (vllm:94-102, 188-265): the device
+    # dequant kernel + a library GEMM in bf16, against the FP64 oracle and
+    # the reference safe path restated on the CPU
+    import types
+    from mxfp4_amd import vllm_adapter as va
+    monkeypatch.setattr(va, "_IMPL", "reference")
+    w13, s13, w2, s2 = layer_weights
+    layer = types.SimpleNamespace(activation="silu", w13_weight=cuda(w13),
+                                  w13_weight_scale=cuda(s13), w2_weight=cuda(w2),
+                                  w2_weight_scale=cuda(s2))
+    m = 6
+    x = rand_act(73, (m, 2048))
+    w, ids = _route(m, 128, 8, 74)
+    y = va._moe_apply(None, layer, cuda(x), cuda(w), cuda(ids))
+    assert y.shape == (m, 2048) and y.dtype == torch.bfloat16
+    oracle, routes = O.moe_layer_fp64(x.float().numpy(), w13, s13, w2, s2, w.numpy(),
+                                      ids.numpy(), return_routes=True)
+    t = torch.from_numpy
+    safe = O.moe_layer_safe(x, t(w13), t(s13), t(w2), t(s2), w, ids)
+    _same_numerics_as_reference(y, safe, oracle, "vllm reference path, moe")
+    dense = types.SimpleNamespace(weight_packed=cuda(w13[5]), weight_scale=cuda(s13[5]))
+    bias = rand_act(75, (1536,))
+    xd = rand_act(76, (2, 3, 2048))
+    yd = va._dense_apply_weights(None, dense, cuda(xd), cuda(bias))
+    assert yd.shape == (2, 3, 1536)
+    od = O.linear_fp64(xd.reshape(6, 2048).float().numpy(), w13[5], s13[5],
+                       bias.float().numpy())
+    _same_numerics_as_reference(yd.reshape(6, 1536),
+                                O.linear_safe(xd, w13[5], s13[5], bias).reshape(6, 1536), od,
+                                "vllm reference path, dense")
+
+
+def _same_numerics_as_reference(y, safe, oracle, what):
+    """The debug path is the reference's own composition (every intermediate
+    rounded to bf16), so its bar is the reference's: its error against the
+    FP64 oracle no worse than the safe path's restated on the CPU (x1.1), and
+    the two within a few bf16 steps of each other (only the BLAS summation
+    order differs)."""
+    y = y.float().cpu().numpy()
+    r = safe.float().cpu().numpy()
+    e, er = O.parity_errors(y, oracle), O.parity_errors(r, oracle)
+    assert e["norm_rel"] <= 1.1 * er["norm_rel"] + 1e-4, (what, e, er)
+    gap = np.linalg.norm(y - r) / np.linalg.norm(r)
+    assert gap <= 1e-2, (what, gap)
+
+
 def test_moe_layer_hidden_not_multiple_of_128():
     # hidden 1056 (K % 128 == 32 for gate_up): routed blocks of 64 go to the
     # register-staged tiled kernel; inter 320 keeps the down GEMM on it too

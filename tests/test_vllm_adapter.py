@@ -3,23 +3,29 @@ classes and layers: what it patches (vllm:268-275), the weight renames of
 process_weights_after_loading (vllm:68-70, 215-230), the implementation switch
 (vllm:28-36), and that apply / apply_weights hand the layer's tensors to
 linear_mxfp4_soft / moe_layer (recorded here; the operators themselves are
-covered by the GPU tests).  vLLM is not installed in this image."""
+covered by the GPU tests), or under MXFP4_IMPLEMENTATION=reference compose
+the debug path (vllm:94-102, 188-265; here with the oracle's dequant in place
+of the device kernel).  vLLM is not installed in this image."""
 
 from __future__ import annotations
 
 import types
 
+import numpy as np
 import pytest
 import torch
 
+from _helpers import rand_act, rand_mxfp4
 from mxfp4_amd import vllm_adapter as va
+from oracle import mxfp4_oracle as O
 
 
 @pytest.fixture(autouse=True)
 def _restore_backend_switch(monkeypatch):
-    # install() sets MXFP4_GFX936_BACKEND for the operators; monkeypatch
-    # restores it after each test
+    # install() sets MXFP4_GFX936_BACKEND for the operators and records the
+    # implementation; monkeypatch restores both after each test
     monkeypatch.setenv("MXFP4_GFX936_BACKEND", "safe")
+    monkeypatch.setattr(va, "_IMPL", None)
 
 
 class _Dense:
@@ -40,15 +46,21 @@ def test_install_patches_both_schemes(monkeypatch, capsys):
     assert "MXFP4_GFX950_ADAPTER_ACTIVE" in capsys.readouterr().out
 
 
-@pytest.mark.parametrize("impl,ok", [("safe", True), ("triton", True), ("reference", False),
-                                     ("bf16", False), ("cuda", False)])
-def test_implementation_switch(monkeypatch, impl, ok):
+@pytest.mark.parametrize("impl,expect", [("safe", "safe"), ("triton", "triton"),
+                                         ("reference", "reference"), ("bf16", "reference"),
+                                         ("cuda", None)])
+def test_implementation_switch(monkeypatch, impl, expect):
+    # vllm:28-36: bf16 is an alias of reference, the operators' backend
+    # switch is triton only for triton
     monkeypatch.setenv("MXFP4_IMPLEMENTATION", impl)
-    if ok:
-        assert va.install(_Dense, _MoE) == impl
-    else:
-        with pytest.raises(ValueError):
+    if expect is None:
+        with pytest.raises(ValueError, match="unknown MXFP4 implementation"):
             va.install(_Dense, _MoE)
+    else:
+        assert va.install(_Dense, _MoE) == expect
+        assert va._IMPL == expect
+        import os
+        assert os.environ["MXFP4_GFX936_BACKEND"] == ("triton" if expect == "triton" else "safe")
 
 
 def test_install_without_vllm_says_so(monkeypatch):
@@ -117,3 +129,33 @@ def test_apply_paths_call_the_operators(monkeypatch):
     moe.activation = "gelu"
     with pytest.raises(NotImplementedError, match="silu"):
         va._moe_apply(object(), moe, "x", "tw", "ti")
+
+
+def test_reference_debug_path_composition(monkeypatch):
+    # MXFP4_IMPLEMENTATION=reference on CPU tensors, with the oracle's
+    # dequant (soft:277-307 in torch) standing in for the device kernel:
+    # the dense path is x @ dequant(W).T + bias and the MoE path the layer
+    # composed over the per-expert loop -- the oracle's own restatements of
+    # the same reference functions give the same bits
+    monkeypatch.setattr(va, "dequant_mxfp4", lambda p, s, dt: O.dequant_safe(p, s, dt))
+    monkeypatch.setattr(va, "_IMPL", "reference")
+    rng = np.random.default_rng(91)
+    w, ws = rand_mxfp4(rng, (48,), 128)
+    x = rand_act(92, (3, 5, 128))
+    bias = rand_act(93, (48,))
+    dense = types.SimpleNamespace(weight_packed=torch.from_numpy(w),
+                                  weight_scale=torch.from_numpy(ws))
+    y = va._dense_apply_weights(object(), dense, x, bias)
+    assert y.shape == (3, 5, 48) and y.dtype == torch.bfloat16
+    assert torch.equal(y, O.linear_safe(x, w, ws, bias))
+    e, hidden, inter, m, top_k = 6, 64, 32, 7, 3
+    w13, s13 = (torch.from_numpy(a) for a in rand_mxfp4(rng, (e, 2 * inter), hidden))
+    w2, s2 = (torch.from_numpy(a) for a in rand_mxfp4(rng, (e, hidden), inter))
+    xm = rand_act(94, (m, hidden))
+    tw, ti = torch.topk(torch.softmax(torch.randn(m, e, generator=torch.Generator().manual_seed(95)),
+                                      -1), top_k, dim=-1)
+    moe = types.SimpleNamespace(activation="silu", w13_weight=w13, w13_weight_scale=s13,
+                                w2_weight=w2, w2_weight_scale=s2)
+    z = va._moe_apply(object(), moe, xm, tw, ti)
+    assert z.shape == (m, hidden) and z.dtype == torch.bfloat16
+    assert torch.equal(z, O.moe_layer_safe(xm, w13, s13, w2, s2, tw, ti))
