@@ -78,11 +78,15 @@ def assert_layer_parity(y, oracle, ref, what="", routes=None, fmt="bf16"):
 
     Bars: norm-wise <= 2e-3 (or, where the output format alone costs more,
     no worse than the oracle correctly rounded to ``fmt``, x1.1) and no
-    worse than the reference safe path (x1.1); elementwise <= 1e-2 for all
-    but 1e-3 of the elements, and every element within 1e-2 or within one
-    ``fmt`` step per route value (``routes``: the oracle's rounded
-    per-route outputs [M, top_k, H]) plus one of the output.  Without
-    ``routes``, elementwise no worse than the reference."""
+    worse than the reference safe path (x1.1; below a tenth of 2e-3 both
+    sit at the rounding-flip noise of the same rounding points and this leg
+    is not applied); elementwise <= 1e-2 for all but 1e-3 of the elements,
+    and every element within 1e-2, or within one ``fmt`` step per route
+    value (``routes``: the oracle's rounded per-route outputs
+    [M, top_k, H]) plus one of the output, or no further from the oracle
+    than the reference plus that budget (a gate / up / h value one step
+    apart moves a route by more than its own step, for the reference as
+    for us).  Without ``routes``, elementwise no worse than the reference."""
     y = y.float().cpu().numpy() if isinstance(y, torch.Tensor) else np.asarray(y)
     r = ref.float().cpu().numpy() if isinstance(ref, torch.Tensor) else np.asarray(ref)
     e = O.parity_errors(y, oracle)
@@ -94,7 +98,7 @@ def assert_layer_parity(y, oracle, ref, what="", routes=None, fmt="bf16"):
     frac = float(np.mean(rel > O.ELEM_TOL))
     if routes is not None:
         budget = O.format_ulp(routes, fmt).sum(axis=1) + O.format_ulp(o, fmt)
-        bad = (rel > O.ELEM_TOL) & (diff > budget)
+        bad = (rel > O.ELEM_TOL) & (diff > budget) & (diff > np.abs(r - o) + budget)
         assert not bad.any(), (
             f"{what} {int(bad.sum())} elements beyond {O.ELEM_TOL} and beyond one {fmt} step per "
             f"route (max elementwise {e['elem_rel']:.3e})")
@@ -104,7 +108,7 @@ def assert_layer_parity(y, oracle, ref, what="", routes=None, fmt="bf16"):
     norm_tol = max(O.NORM_TOL, 1.1 * _format_floor(o, fmt))
     assert e["norm_rel"] <= norm_tol, f"{what} norm-wise {e['norm_rel']:.3e} > {norm_tol:.3e}"
     assert frac <= 1e-3, f"{what} {frac:.2e} of elements beyond {O.ELEM_TOL}"
-    assert e["norm_rel"] <= er["norm_rel"] * 1.1 + 1e-7, (
+    assert e["norm_rel"] <= max(er["norm_rel"] * 1.1 + 1e-7, 0.1 * O.NORM_TOL), (
         f"{what} worse than the reference: {e['norm_rel']:.3e} vs {er['norm_rel']:.3e}")
     return e, er
 
@@ -247,3 +251,43 @@ def prepack_layout_np(packed: np.ndarray, scales: np.ndarray):
     ops = ((s.astype(np.uint16) << 7) | np.uint16(0x40)).astype(np.uint16)
     sc = ops.reshape(e, g, 16, nk, 2).transpose(0, 1, 3, 2, 4)
     return np.ascontiguousarray(nib), np.ascontiguousarray(sc)
+
+
+def assert_layer_blocks(y, o, ref, routes, what, row_block=128):
+    """The MoE layer bar (tests/_helpers.assert_layer_parity) on whole
+    outputs, per block of ``row_block`` tokens: norm-wise <= NORM_TOL and no
+    worse than the reference per block; every element within ELEM_TOL or
+    within one bf16 step per route value (``routes``, the oracle's rounded
+    per-route outputs) plus one of the output; <= ELEM_TOL on all but 1e-3
+    of the elements."""
+    y2, o2, r2 = y.double(), o.double(), ref.double()
+    floor = 1e-3 * o2.square().mean().sqrt()
+    diff = (y2 - o2).abs()
+    rel = diff / o2.abs().clamp(min=floor)
+    budget = (O.format_ulp(routes.double().cpu().numpy(), "bf16").sum(axis=1)
+              + O.format_ulp(o2.cpu().numpy(), "bf16"))
+    budget = torch.from_numpy(budget).to(diff.device)
+    # an upstream rounding flip (gate, up or h one bf16 step apart) moves a
+    # route by more than its own step; the reference composition takes such
+    # flips too, so an element no further from the oracle than the
+    # reference's (plus the budget) passes
+    bad = (rel > O.ELEM_TOL) & (diff > budget) & (diff > (r2 - o2).abs() + budget)
+    if bool(bad.any()):
+        i, j = (int(v) for v in bad.nonzero()[0])
+        raise AssertionError(
+            f"{what} {int(bad.sum())} elements beyond {O.ELEM_TOL} and one bf16 step per route "
+            f"(max {rel.max():.3e}); first at [{i}, {j}]: y {y2[i, j].item():.6g} oracle "
+            f"{o2[i, j].item():.6g} reference {r2[i, j].item():.6g} budget {budget[i, j]:.3g} "
+            f"routes {routes[i, :, j].double().cpu().numpy().tolist()}")
+    frac = (rel > O.ELEM_TOL).double().mean().item()
+    assert frac <= 1e-3, f"{what} {frac:.2e} of elements beyond {O.ELEM_TOL}"
+    nb = y2.shape[0] // row_block
+    on = o2[:nb * row_block].reshape(nb, -1).norm(dim=1)
+    err = (y2 - o2)[:nb * row_block].reshape(nb, -1).norm(dim=1) / on
+    rerr = (r2 - o2)[:nb * row_block].reshape(nb, -1).norm(dim=1) / on
+    assert err.max() <= O.NORM_TOL, f"{what} norm-wise {err.max():.3e}"
+    # below a tenth of the bar both sit at the rounding-flip noise of the
+    # same rounding points, where "no worse" is a coin toss
+    ok = (err <= 1.1 * rerr + 1e-7) | (err <= 0.1 * O.NORM_TOL)
+    assert bool(ok.all()), (f"{what} worse than the reference in a block: "
+                            f"{err[~ok][0].item():.3e} vs {rerr[~ok][0].item():.3e}")

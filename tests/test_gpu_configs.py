@@ -29,8 +29,9 @@ import torch
 import mxfp4_amd as mx
 from oracle import mxfp4_oracle as O
 
-from _helpers import (assert_layer_parity, assert_parity, assert_rows_parity, cuda, fp32_gemm,
-                      moe_layer_device, rand_act, rand_mxfp4, safe_linear_device)
+from _helpers import (assert_layer_blocks, assert_layer_parity, assert_parity, assert_rows_parity,
+                      cuda, fp32_gemm, moe_layer_device, rand_act, rand_mxfp4,
+                      safe_linear_device)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::RuntimeWarning")]
 
@@ -330,32 +331,6 @@ def _route(m, seed):
     return (w / w.sum(-1, keepdim=True)).float(), ids
 
 
-def _assert_layer_blocks(y, o, ref, routes, what, row_block=128):
-    """The MoE layer bar (tests/_helpers.assert_layer_parity) on whole
-    outputs, per block of ``row_block`` tokens: norm-wise <= NORM_TOL and no
-    worse than the reference per block; every element within ELEM_TOL or
-    within one bf16 step per route value (``routes``, the oracle's rounded
-    per-route outputs) plus one of the output; <= ELEM_TOL on all but 1e-3
-    of the elements."""
-    y2, o2, r2 = y.double(), o.double(), ref.double()
-    floor = 1e-3 * o2.square().mean().sqrt()
-    diff = (y2 - o2).abs()
-    rel = diff / o2.abs().clamp(min=floor)
-    budget = (O.format_ulp(routes.double().cpu().numpy(), "bf16").sum(axis=1)
-              + O.format_ulp(o2.cpu().numpy(), "bf16"))
-    bad = (rel > O.ELEM_TOL) & (diff > torch.from_numpy(budget).to(diff.device))
-    assert not bool(bad.any()), (f"{what} {int(bad.sum())} elements beyond {O.ELEM_TOL} and one "
-                                 f"bf16 step per route (max {rel.max():.3e})")
-    frac = (rel > O.ELEM_TOL).double().mean().item()
-    assert frac <= 1e-3, f"{what} {frac:.2e} of elements beyond {O.ELEM_TOL}"
-    nb = y2.shape[0] // row_block
-    on = o2[:nb * row_block].reshape(nb, -1).norm(dim=1)
-    err = (y2 - o2)[:nb * row_block].reshape(nb, -1).norm(dim=1) / on
-    rerr = (r2 - o2)[:nb * row_block].reshape(nb, -1).norm(dim=1) / on
-    assert err.max() <= O.NORM_TOL, f"{what} norm-wise {err.max():.3e}"
-    assert bool((err <= 1.1 * rerr + 1e-7).all()), f"{what} worse than the reference in a block"
-
-
 @pytest.mark.parametrize("m", [512, 4096])
 def test_moe_layer_whole_output(m, layer_weights_full):
     w13, s13, w2, s2 = layer_weights_full
@@ -374,7 +349,7 @@ def test_moe_layer_whole_output(m, layer_weights_full):
     # sum lands on the other side of a bf16 rounding boundary
     e = O.parity_errors(o32[torch.from_numpy(rows).cuda()].cpu().numpy(), oracle)
     assert e["norm_rel"] <= 2e-4, e
-    _assert_layer_blocks(y, o32, ref, routes, what=f"moe layer m={m}")
+    assert_layer_blocks(y, o32, ref, routes, what=f"moe layer m={m}")
 
 
 @pytest.mark.parametrize("m,top_k", [(2000, 4), (300, 8)])
@@ -396,7 +371,7 @@ def test_moe_layer_skewed_routing_whole_output(m, top_k):
     d13, d2 = _dequant_experts(w13, s13), _dequant_experts(w2, s2)
     o32, routes = moe_layer_device(xd, d13, d2, wd, idd, "f32", return_routes=True)
     ref = moe_layer_device(xd, d13, d2, wd, idd, "ref")
-    _assert_layer_blocks(y, o32, ref, routes, what=f"skewed moe layer m={m} top_k={top_k}",
+    assert_layer_blocks(y, o32, ref, routes, what=f"skewed moe layer m={m} top_k={top_k}",
                          row_block=100)
 
 
