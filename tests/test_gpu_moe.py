@@ -182,11 +182,13 @@ def test_aiter_entry_uses_metadata(block_m):
 
 
 @pytest.mark.parametrize("block_m", [64, 128, 256])
-def test_aiter_entry_w4a4_metadata(block_m):
+@pytest.mark.parametrize("k", [256, 1024])
+def test_aiter_entry_w4a4_metadata(block_m, k):
     # packed MXFP4 activations through caller metadata, with an expert -1
-    # block and enough routes to fill several row blocks per expert
+    # block and enough routes to fill several row blocks per expert; K = 1024
+    # (a multiple of 512) stages four stages of scales per load
     rng = np.random.default_rng(block_m + 1)
-    m, k, n, e, top_k = 300, 256, 320, 4, 2
+    m, n, e, top_k = 300, 320, 4, 2
     wp, ws = rand_mxfp4(rng, (e, n), k)
     ap, asc = O.quant_mxfp4_ties_away(rand_act(block_m + 7, (m, k)).float().numpy())
     w, ids = _route(m, e, top_k, 200 + block_m)

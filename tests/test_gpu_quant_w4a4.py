@@ -95,12 +95,16 @@ def test_w4a4_linear(m, k, n, out_dtype):
 
 
 @pytest.mark.parametrize("m,n,out_dtype", [(4096, 4096, torch.bfloat16), (2048, 2048, torch.float16),
-                                           (2048, 4096, torch.float32), (1000, 4100, torch.bfloat16)],
-                         ids=["256x256", "128x128", "f32_out", "partial"])
-def test_w4a4_tile_configs(m, n, out_dtype):
+                                           (2048, 4096, torch.float32), (1000, 4100, torch.bfloat16),
+                                           (4096, 4096, torch.float32), (4000, 4100, torch.float16)],
+                         ids=["256x256", "128x128", "f32_out", "partial", "f32_256x256",
+                              "partial_256x256"])
+@pytest.mark.parametrize("k", [256, 1536], ids=["scale_stage", "scale_group4"])
+def test_w4a4_tile_configs(m, n, out_dtype, k):
     # grids large enough for the 256 x 256 (>= 256 tiles) / 128 x 128 tiles,
-    # FP32 output, and partial row / column tiles; checked on sampled rows
-    k = 256
+    # FP32 output, and partial row / column tiles; checked on sampled rows.
+    # K = 256 stages the scales one 128-deep stage at a time, K = 1536
+    # (a multiple of 512) four stages per 16-byte load.
     a = rand_act(m + 1, (m, k)).float().numpy()
     w = (rand_act(n + 2, (n, k)).float() * 0.02).numpy()
     ap, asc = O.quant_mxfp4_rne(a)
