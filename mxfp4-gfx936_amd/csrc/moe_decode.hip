@@ -43,17 +43,15 @@ struct DownArgs {
   int32_t cw;   // output columns per workgroup: 16, or 8 when 16 would leave CUs idle
 };
 
-__device__ __forceinline__ int route_expert(const DownArgs& a, int64_t r) {
-  const int64_t e = a.ids64 ? static_cast<const int64_t*>(a.ids)[r]
-                            : (int64_t) static_cast<const int32_t*>(a.ids)[r];
-  return (e >= 0 && e < a.num_experts) ? (int)e : -1;
-}
-
 template <typename T, int RW, int WK, int U>
 __global__ __launch_bounds__(RW * WK * 64) void moe_down_topk(DownArgs a) {
   typedef typename Decode<T>::vec8 V8;
   static_assert(U == 2 || U == 4, "scale loads cover 2 or 4 units");
   __shared__ f32x4 red[WK][64];
+  // the tile's route weights (entries 0 .. 15; one slot per lane of the
+  // direct-to-LDS load), loaded with the expert ids before the weight
+  // stream so the combine needs no global loads and no registers
+  __shared__ __attribute__((aligned(256))) float route_wt[64];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
@@ -74,6 +72,7 @@ __global__ __launch_bounds__(RW * WK * 64) void moe_down_topk(DownArgs a) {
   // expert of each route of the tile: lane i loads route r0 + i's id (raw
   // words, one load), each wave reads its routes' ids from those lanes
   int e[kRG];
+  uint64_t valid;  // bit i: route r0 + i has an expert in [0, E)
   {
     const int esz = a.ids64 ? 8 : 4;
     const i32x4 rI = make_rsrc(a.ids, (uint32_t)(routes * esz));
@@ -91,6 +90,12 @@ __global__ __launch_bounds__(RW * WK * 64) void moe_down_topk(DownArgs a) {
     const int ok = (lane < nrows && id >= 0 && id < a.num_experts) ? (int)id : -1;
 #pragma unroll
     for (int q = 0; q < kRG; ++q) e[q] = __builtin_amdgcn_readlane(ok, (rw * kRG + q) & 63);
+    valid = __ballot(ok >= 0);
+    if (wave == 0) {
+      const i32x4 rW = make_rsrc(a.route_w, (uint32_t)(routes * 4));
+      llvm_amdgcn_raw_buffer_load_lds(rW, lds_ptr(reinterpret_cast<uint8_t*>(route_wt)), 4,
+                                      lane < nrows ? (int)((r0 + lane) * 4) : (int)kOOB, 0, 0, 0);
+    }
   }
   const int64_t b_n = a.inter / 2, bs_n = a.inter / 32;
   const int64_t b_e = (int64_t)a.hidden * b_n, bs_e = (int64_t)a.hidden * bs_n;
@@ -174,6 +179,7 @@ __global__ __launch_bounds__(RW * WK * 64) void moe_down_topk(DownArgs a) {
   for (int q = 1; q < kRG; ++q)
     if ((c16 % kRG) == q) res = acc[q];
   if (c16 / kRG == rw) red[wk][lane] = res;
+  wait_vmcnt<0>();  // route_wt has landed
   __syncthreads();
 
   for (int idx = threadIdx.x; idx < tpt * 16; idx += RW * WK * 64) {
@@ -185,13 +191,12 @@ __global__ __launch_bounds__(RW * WK * 64) void moe_down_topk(DownArgs a) {
     float total = 0.f;
     for (int k = 0; k < a.top_k; ++k) {
       const int rho = tl * a.top_k + k;
-      const int64_t r = r0 + rho;
-      if (route_expert(a, r) < 0) continue;
+      if (!((valid >> rho) & 1)) continue;  // expert outside [0, E)
       const int l = (c >> 2) * 16 + rho;
       float v = 0.f;
 #pragma unroll
       for (int w = 0; w < WK; ++w) v += red[w][l][c & 3];
-      total += to_f32(from_f32<T>(v * a.route_w[r]));
+      total += to_f32(from_f32<T>(v * route_wt[rho]));
     }
     static_cast<T*>(a.out)[t * a.hidden + blockIdx.x * cw + c] = from_f32<T>(total);
   }
