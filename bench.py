@@ -267,6 +267,27 @@ def moe_probe() -> int:
     return 0
 
 
+def w4a4_probe() -> int:
+    """W4A4 launches for trace and counter runs: packed MXFP4 activations x
+    packed MXFP4 weights at M=8192, K=N=4096, bf16 out,
+    an untimed clock ramp, then 20 launches."""
+    import torch
+
+    import mxfp4_amd as mx
+    mx._lib.load()
+    m, k, n = 8192, 4096, 4096
+    a = randn_bf16(4, (m, k))
+    wt = randn_bf16(5, (n, k)).float() * 0.02
+    ap, asc = mx.dynamic_mxfp4_quant(a, "rne")
+    wp, wsc = mx.dynamic_mxfp4_quant(wt, "rne")
+    ramp_clocks(lambda: mx.linear_mxfp4_w4a4(ap, asc, wp, wsc))
+    for _ in range(20):
+        mx.linear_mxfp4_w4a4(ap, asc, wp, wsc)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "w4a4", "m": m, "k": k, "n": n}))
+    return 0
+
+
 def data_probe() -> int:
     """Steady-clock time of the headline GEMM on random inputs (the bench's)
     and on all-zero / constant ones.  The kernel and the work are the same;
@@ -642,6 +663,8 @@ def main() -> int:
                     help="time the headline GEMM on random vs zero / constant inputs")
     ap.add_argument("--moe-probe", action="store_true",
                     help="only run MoE layer prefill launches for trace runs")
+    ap.add_argument("--w4a4-probe", action="store_true",
+                    help="only run W4A4 launches (8192 x 4096 x 4096) for trace / counter runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -656,6 +679,8 @@ def main() -> int:
         return data_probe()
     if args.moe_probe:
         return moe_probe()
+    if args.w4a4_probe:
+        return w4a4_probe()
 
     import numpy as np
     import torch
