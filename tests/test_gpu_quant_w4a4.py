@@ -116,6 +116,25 @@ def test_w4a4_tile_configs(m, n, out_dtype, k):
     assert_parity(y[torch.from_numpy(rows).cuda()], oracle, what=f"w4a4 {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("m,n", [(5000, 9000), (4000, 4100)], ids=["720_tiles", "partial"])
+def test_w4a4_multi_round_grid(m, n):
+    # more 256 x 256 tiles than CUs on a dense grid (K % 512 == 0: grouped
+    # scales, 256-deep stages): 720 / 272 tiles in rounds of 256
+    # workgroups, partial row and column tiles; sampled rows, the last one
+    # included
+    k = 1024
+    a = rand_act(m + 3, (m, k)).float().numpy()
+    w = (rand_act(n + 4, (n, k)).float() * 0.02).numpy()
+    ap, asc = O.quant_mxfp4_rne(a)
+    wp, wsc = O.quant_mxfp4_rne(w)
+    y = mx.linear_mxfp4_w4a4(cuda(ap), cuda(asc), cuda(wp), cuda(wsc), torch.bfloat16)
+    assert y.shape == (m, n)
+    rows = np.sort(np.concatenate([np.random.default_rng(m).choice(m - 1, 40, replace=False),
+                                   [m - 1]]))
+    oracle = O.dequant_values(ap[rows], asc[rows], "f32") @ O.dequant_values(wp, wsc, "f32").T
+    assert_parity(y[torch.from_numpy(rows).cuda()], oracle, what=f"w4a4 multi-round {m}x{k}x{n}")
+
+
 def test_w4a4_baseline_shape_sampled():
     # M=8192, K=4096, N=4096 (checked on sampled rows)
     m, k, n = 8192, 4096, 4096
