@@ -135,6 +135,37 @@ def test_w4a4_multi_round_grid(m, n):
     assert_parity(y[torch.from_numpy(rows).cuda()], oracle, what=f"w4a4 multi-round {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("which", ["a", "w"])
+def test_w4a4_scale_rows_off_16_bytes(which):
+    # scale rows that start 4 bytes past a 16-byte boundary take the
+    # per-stage-scale kernel (3 stages of 128) instead of the grouped-scale
+    # one (2 stages of 256); both accumulate in the same K order, so the
+    # outputs are bitwise equal; and both match the oracle on sampled rows
+    m, k, n = 4096, 1024, 4096
+    a = rand_act(11, (m, k)).float().numpy()
+    w = (rand_act(12, (n, k)).float() * 0.02).numpy()
+    ap, asc = O.quant_mxfp4_rne(a)
+    wp, wsc = O.quant_mxfp4_rne(w)
+    ap_d, asc_d, wp_d, wsc_d = cuda(ap), cuda(asc), cuda(wp), cuda(wsc)
+    ref = mx.linear_mxfp4_w4a4(ap_d, asc_d, wp_d, wsc_d)
+
+    def off4(t):
+        buf = torch.zeros(t.numel() + 16, dtype=torch.uint8, device="cuda")
+        v = buf[4:4 + t.numel()].view(t.shape)
+        v.copy_(t)
+        assert v.is_contiguous() and v.data_ptr() % 16 == 4
+        return v
+
+    if which == "a":
+        y = mx.linear_mxfp4_w4a4(ap_d, off4(asc_d), wp_d, wsc_d)
+    else:
+        y = mx.linear_mxfp4_w4a4(ap_d, asc_d, wp_d, off4(wsc_d))
+    assert torch.equal(y, ref)
+    rows = np.sort(np.random.default_rng(13).choice(m, 32, replace=False))
+    oracle = O.dequant_values(ap[rows], asc[rows], "f32") @ O.dequant_values(wp, wsc, "f32").T
+    assert_parity(y[torch.from_numpy(rows).cuda()], oracle, what=f"w4a4 scales off 16 ({which})")
+
+
 def test_w4a4_baseline_shape_sampled():
     # M=8192, K=4096, N=4096 (checked on sampled rows)
     m, k, n = 8192, 4096, 4096
