@@ -136,12 +136,14 @@ def test_w4a4_multi_round_grid(m, n):
 
 
 @pytest.mark.parametrize("which", ["a", "w"])
-def test_w4a4_scale_rows_off_16_bytes(which):
+@pytest.mark.parametrize("m,n", [(4096, 4096), (2048, 2048)], ids=["256x256", "128x128"])
+def test_w4a4_scale_rows_off_16_bytes(which, m, n):
     # scale rows that start 4 bytes past a 16-byte boundary take the
     # per-stage-scale kernel (3 stages of 128) instead of the grouped-scale
     # one (2 stages of 256); both accumulate in the same K order, so the
     # outputs are bitwise equal; and both match the oracle on sampled rows
-    m, k, n = 4096, 1024, 4096
+    # (256 x 256 tiles at 4096 x 4096, 128 x 128 at 2048 x 2048)
+    k = 1024
     a = rand_act(11, (m, k)).float().numpy()
     w = (rand_act(12, (n, k)).float() * 0.02).numpy()
     ap, asc = O.quant_mxfp4_rne(a)
@@ -163,7 +165,7 @@ def test_w4a4_scale_rows_off_16_bytes(which):
     assert torch.equal(y, ref)
     rows = np.sort(np.random.default_rng(13).choice(m, 32, replace=False))
     oracle = O.dequant_values(ap[rows], asc[rows], "f32") @ O.dequant_values(wp, wsc, "f32").T
-    assert_parity(y[torch.from_numpy(rows).cuda()], oracle, what=f"w4a4 scales off 16 ({which})")
+    assert_parity(y[torch.from_numpy(rows).cuda()], oracle, what=f"w4a4 scales off 16 ({which}, {m}x{n})")
 
 
 def test_w4a4_baseline_shape_sampled():
