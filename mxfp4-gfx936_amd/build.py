@@ -24,6 +24,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 OBJ_DIR = os.path.join(HERE, "_build")
+GEN_DIR = os.path.join(OBJ_DIR, "gen")  # generated sources (silu_table.inc)
 LIB = os.path.join(HERE, "mxfp4_amd", "libmxfp4_gfx950.so")
 # measurement aid for bench.py (a plain HBM read), kept out of the library
 PROBE_SRC = os.path.join(CSRC, "probe", "read_floor.hip")
@@ -39,6 +40,7 @@ CFLAGS = [
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",
+    f"-I{GEN_DIR}",
 ]
 
 
@@ -61,7 +63,10 @@ def _compile(src: str, verbose: bool) -> str:
 
 def build(verbose: bool = False) -> str:
     """Compile all HIP sources and link the shared library; returns its path."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
+    os.makedirs(GEN_DIR, exist_ok=True)
+    sys.path.insert(0, HERE)
+    import silu_table  # the SiLU lookup tables of csrc/silu.h
+    silu_table.write_inc(os.path.join(GEN_DIR, "silu_table.inc"))
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")

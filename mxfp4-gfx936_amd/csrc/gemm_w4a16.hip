@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "gemm.h"
+#include "silu.h"
 
 namespace mx {
 namespace {
@@ -60,7 +61,7 @@ __device__ __forceinline__ void store_out(const GemmArgs& g, const RowInfo& r, i
     // FP32 and rounded to T, the product rounded to T.
     const T gb = from_f32<T>(v0 * alpha);
     const T ub = from_f32<T>(v1 * alpha);
-    const T sb = from_f32<T>(silu_f32(to_f32(gb)));
+    const T sb = silu_round<T>(gb);
     *cp = from_f32<T>(to_f32(sb) * to_f32(ub));
   }
 }

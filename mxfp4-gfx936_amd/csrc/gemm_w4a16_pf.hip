@@ -32,6 +32,7 @@
 #include <atomic>
 
 #include "gemm.h"
+#include "silu.h"
 
 namespace mx {
 namespace {
@@ -424,7 +425,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
               // in FP32 rounded to T, the product rounded to T (below)
               const T gb = from_f32<T>(acc[fm][fn][i] * alpha);
               const T ub = from_f32<T>(acc[fm][fn + 1][i] * alpha);
-              const T sb = from_f32<T>(silu_f32(to_f32(gb)));
+              const T sb = silu_round<T>(gb);
               h[i] = to_f32(sb) * to_f32(ub);
             }
             *reinterpret_cast<uint2*>(crow + tcol * 2) =
@@ -803,7 +804,7 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
             // vllm:249-252 on tensors of T (as in w4a16_pf)
             const T gb = from_f32<T>(acc[fm][fn][i] * alpha);
             const T ub = from_f32<T>(acc[fm][fn + 1][i] * alpha);
-            const T sb = from_f32<T>(silu_f32(to_f32(gb)));
+            const T sb = silu_round<T>(gb);
             h[i] = expert >= 0 ? to_f32(sb) * to_f32(ub) : 0.f;
           }
           const uint32_t off =
