@@ -24,7 +24,8 @@ on ``bench.py --traffic-probe`` and recorded in
 profiles/w4a16_pf_qkv_prefill_traffic.md, or null when that file is absent.  ``sweep`` carries the other BASELINE points:
 decode W4A16 GEMV (HBM GB/s, weights rotated over >= 512 MB so the 256 MB
 MALL cannot serve them, launches replayed from a HIP graph), the routed MoE
-layer (us), the soft op with C in FP32 (FP32 MFMA) and bf16, W4A4 on the
+layer (us), the soft op (C bf16 at 512 and 4096 tokens, C FP32 on the FP32
+MFMA at 512) and the AITER entry on caller metadata, W4A4 on the
 block-scaled FP4 MFMA, and the standalone dequant.
 ``cpu_baseline`` times the reference safe path (explicit dequant +
 torch.matmul bf16, restated in oracle/) on this host's cores on a bounded
@@ -373,6 +374,57 @@ def linear_bytes(m, n, k, prepacked=False):
     return n * k // 2 + n * k // (16 if prepacked else 32) + 2 * m * k + 2 * m * n
 
 
+def soft_op_cases(mx, torch, np):
+    """(name, call, FLOPs, peak) of the soft-op and AITER-entry rows: BASELINE
+    config 3's gate_up shape (E=128, top-8, K=2048, N=1536), seeded."""
+    e, k, n, top_k = 128, 2048, 1536, 8
+    (wp, wsc), = rand_weights(np.random.default_rng(20260818), (e, n), k)
+    one, ones_e, empty = (torch.ones(1, device="cuda"), torch.ones(e, device="cuda"),
+                          torch.empty(0, device="cuda"))
+    cases = []
+    for m, cdt, name in ((512, torch.bfloat16, "bf16"), (4096, torch.bfloat16, "bf16"),
+                         (512, torch.float32, "f32")):
+        a = randn_bf16(20260819, (m, k))
+        g = torch.Generator().manual_seed(20260820)
+        tw, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
+        tw, ids = tw.cuda(), ids.cuda()
+        C = torch.empty((m, top_k, n), dtype=cdt, device="cuda")
+        fl = 2.0 * m * top_k * n * k
+        peak = FP32_PEAK_TFLOPS if cdt == torch.float32 else BF16_PEAK_TFLOPS
+        cases.append((f"fused_moe_soft_c{name}_m{m}",
+                      lambda a=a, C=C, tw=tw, ids=ids: mx.fused_moe_mxfp4_soft(
+                          a, wp, C, one, ones_e, None, wsc, tw, ids, empty, empty, empty, True,
+                          top_k, False, False), fl, peak))
+        if m == 512 and cdt == torch.bfloat16:
+            for bm in (32, 64):
+                srt, eid, npp = mx.make_routing_device(ids, e, bm)
+                cases.append((f"aiter_fused_moe_bm{bm}_m{m}",
+                              lambda a=a, C=C, tw=tw, ids=ids, srt=srt, eid=eid, npp=npp, bm=bm:
+                              mx.fused_moe_mxfp4(a, wp, C, one, ones_e, None, wsc, tw, ids, srt,
+                                                 eid, npp, True, top_k, False, False,
+                                                 {"BLOCK_SIZE_M": bm}, torch.bfloat16),
+                              fl, BF16_PEAK_TFLOPS))
+    return cases
+
+
+def soft_probe() -> int:
+    """Soft-op and AITER-entry launches for trace runs (the soft_op_cases
+    rows), each after an untimed clock ramp, 20 calls."""
+    import numpy as np
+    import torch
+
+    import mxfp4_amd as mx
+    mx._lib.load()
+    for key, fn, _, _ in soft_op_cases(mx, torch, np):
+        ramp_clocks(fn)
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        log(f"soft probe {key} done")
+    print(json.dumps({"probe": "soft"}))
+    return 0
+
+
 def sweep(mx, torch, np):
     res = {}
     # --- decode / mid W4A16 (BASELINE config 2)
@@ -448,35 +500,21 @@ def sweep(mx, torch, np):
         log(f"moe m={m}: {res[f'moe_layer_m{m}']}")
     del layer_copies
     torch.cuda.empty_cache()
-    # --- the soft op's FP32 compute path (C fp32, soft:405-407) on the
-    # BASELINE gate_up shape at 512 tokens, beside the same call with C bf16
-    # (each call: device routing, C zero-fill, the routed GEMM)
-    e, k, n, m = 128, 2048, 1536, 512
-    (wp, wsc), = rand_weights(np.random.default_rng(20260818), (e, n), k)
-    a = randn_bf16(20260819, (m, k))
-    g = torch.Generator().manual_seed(20260820)
-    tw, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
-    tw, ids = tw.cuda(), ids.cuda()
-    one, ones_e, empty = (torch.ones(1, device="cuda"), torch.ones(e, device="cuda"),
-                          torch.empty(0, device="cuda"))
-    for cdt, name, peak in ((torch.float32, "f32", FP32_PEAK_TFLOPS),
-                            (torch.bfloat16, "bf16", BF16_PEAK_TFLOPS)):
-        C = torch.empty((m, top_k, n), dtype=cdt, device="cuda")
-
-        def call():
-            mx.fused_moe_mxfp4_soft(a, wp, C, one, ones_e, None, wsc, tw, ids, empty, empty,
-                                    empty, True, top_k, False, False)
-        # device time from graph replays (the op never synchronises the
-        # host); eager_us adds the Python validation and launch overhead
-        t = time_graph([call] * 4, replays=10)
-        te = time_eager(call, 20, 3)[1]
-        fl = 2.0 * m * top_k * n * k
-        res[f"fused_moe_soft_c{name}_m{m}"] = {
-            "us": round(t * 1e3, 2), "TFLOP/s": round(fl / t / 1e9, 2),
-            "peak_frac": round(fl / t / 1e9 / peak, 4), "peak": peak,
-            "eager_us": round(te * 1e3, 2)}
-        log(f"fused moe soft C {name}: {res[f'fused_moe_soft_c{name}_m{m}']}")
-    del wp, wsc
+    # --- the soft op (soft:379-494) on BASELINE config 3's gate_up shape
+    # (E=128, top-8, K=2048, N=1536): C bf16 at 512 and 4096 tokens, C fp32
+    # (the FP32 compute path, soft:405-407) at 512; each call builds the
+    # routing on the device and writes all of C.  Beside it the AITER entry
+    # (aiter:367-472) on caller metadata of BLOCK_SIZE_M 32 and 64 at 512
+    # tokens (the metadata is built once, outside the timing, as a caller
+    # would pass it in).
+    for key, fn, fl, peak in soft_op_cases(mx, torch, np):
+        t = time_graph([fn] * 4, replays=10)
+        te = time_eager(fn, 20, 3)[1]
+        res[key] = {"us": round(t * 1e3, 2), "TFLOP/s": round(fl / t / 1e9, 2),
+                    "peak_frac": round(fl / t / 1e9 / peak, 4), "peak": peak,
+                    "eager_us": round(te * 1e3, 2)}
+        log(f"{key}: {res[key]}")
+    torch.cuda.empty_cache()
     # --- W4A4, activations/weights quantized with the RNE rule
     m, k, n = 8192, 4096, 4096
     a = randn_bf16(4, (m, k))
@@ -663,6 +701,8 @@ def main() -> int:
                     help="time the headline GEMM on random vs zero / constant inputs")
     ap.add_argument("--moe-probe", action="store_true",
                     help="only run MoE layer prefill launches for trace runs")
+    ap.add_argument("--soft-probe", action="store_true",
+                    help="only run soft-op / AITER-entry launches for trace runs")
     ap.add_argument("--w4a4-probe", action="store_true",
                     help="only run W4A4 launches (8192 x 4096 x 4096) for trace / counter runs")
     args = ap.parse_args()
@@ -681,6 +721,8 @@ def main() -> int:
         return moe_probe()
     if args.w4a4_probe:
         return w4a4_probe()
+    if args.soft_probe:
+        return soft_probe()
 
     import numpy as np
     import torch

@@ -205,6 +205,31 @@ int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_str
                    int block_m, int64_t num_valid, int top_k, void* stream);
 
 /*
+ * fused_moe_mxfp4_soft(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale,
+ * topk_weights, topk_ids, ...) -- soft:379-494, safe semantics, in one call
+ * (the routing metadata arguments, which soft:466 ignores, are not taken).
+ * a, a_mx, b, b_mx, a_scale, b_scale, topk_weights, mul_routed_weight as in
+ * mxfp4_moe_gemm; topk_ids I32/I64 [m, top_k]; c [m, top_k, n] contiguous,
+ * 16-byte aligned, of c_dtype.  Every element of c is written: for each
+ * (t, s) with e = topk_ids[t, s] in [0, num_experts)
+ *   c[t, s, :] = a[t] . dequant(b[e])^T * a_scale[0] * b_scale[e]
+ *                (* topk_weights[t, s] if mul_routed_weight),
+ * FP32 accumulation, one rounding; every other row is zero (soft:476: C is
+ * zero-filled first -- here only the rows no GEMM row covers are written
+ * with zeros, which gives the same C).  Routing is built on the device; no
+ * host synchronisation.  `workspace` (16-byte aligned) must hold
+ * mxfp4_fused_moe_workspace_size bytes.  num_experts <= 1024.
+ */
+int mxfp4_fused_moe_workspace_size(int64_t m, int top_k, int64_t num_experts, int a_dtype,
+                                   int c_dtype, int64_t* bytes);
+int mxfp4_fused_moe(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
+                    const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,
+                    int64_t num_experts, int64_t n, int64_t k, void* c, int c_dtype,
+                    const float* a_scale, const float* b_scale, const float* topk_weights,
+                    int mul_routed_weight, const void* topk_ids, int ids_dtype, int64_t m,
+                    int top_k, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * The vLLM MoE layer, vllm:233-265 (silu only):
  *   gu = moe(x, w13)                  [m, top_k, 2*inter] rounded to x's dtype
  *   h  = silu(gu[..., :inter]) * gu[..., inter:]   (rounded as the reference)

@@ -1030,6 +1030,28 @@ int pf_choose(const GemmArgs& g, int epi) {
     }
     if (best >= 0) return best;
   }
+  // Routed plain GEMMs on the checkpoint layout stage 32 bytes of every
+  // weight row per 64-deep step (a cache line per row and step), so tiles
+  // of few rows and many columns -- the prepacked layout's choices below --
+  // spend their time on weight requests.  Measured (E=128, top-8, routed
+  // GEMM alone, graph replays; K=2048 N=1536 / K=768 N=2048): 128-row
+  // blocks take 128 x 256 (1024 tokens 80.2 / 52.3 vs 128 x 128 87.8 /
+  // 51.3 us; 4096 tokens 235.9 / 146.5 vs 242.5 / 161.0); 32- and 64-row
+  // blocks BM x 128 while those tiles number <= 10 per CU, else BM x 256
+  // (512 tokens, 64-row blocks: 64 x 128 59.0 / 35.9 vs 64 x 256 66.9 /
+  // 39.1; 32-row blocks: 32 x 128 67.7 vs 32 x 256 75.3 and 32 x 512
+  // 117 us; 1024 tokens, down: 64 x 256 49.3 vs 64 x 128 51.9).
+  if (routed && epi == EPI_STORE && !pf_prepacked_usable(g)) {
+    if (allowed(128)) return PF_128x256;
+    const int bm = allowed(64) ? 64 : 32;
+    const int64_t cus = device_cus();
+    const int64_t busy = g.num_experts < g.num_valid ? g.num_experts : g.num_valid;
+    const int64_t blocks = g.num_valid / bm + busy / 2;
+    const int64_t t128 = blocks * ((g.n + 127) / 128);
+    const bool narrow = cus <= 0 || t128 <= 10 * cus;
+    if (bm == 64) return narrow ? PF_64x128 : PF_64x256;
+    return narrow ? PF_32x128 : PF_32x256;
+  }
   if (allowed(128)) {
     const double f256 = fill(256);
     const double f320 = epi == EPI_STORE ? fill(320) : 0.0;

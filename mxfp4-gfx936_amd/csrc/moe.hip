@@ -16,6 +16,7 @@
 // The result is identical to the host loop of vllm:119-146 (ascending
 // experts, ascending route ids inside an expert) for ids in [0, E); other ids
 // are dropped, leaving those rows untouched (soft:476-481: they stay zero).
+#include <algorithm>
 #include <mutex>
 
 #include "gemm.h"
@@ -39,9 +40,20 @@ constexpr int kMaxExperts = 1024;
 // three-launch path).
 constexpr int kSingleExperts = 256;
 
+// Expert of a route: its id when in [0, num_experts), else drop_to.  With
+// drop_to = -1 the route is dropped (in no block; its output rows are not
+// written).  The fused soft op passes num_experts = E + 1 and drop_to = E:
+// dropped routes then gather in blocks of the extra expert E, which the
+// GEMMs (experts outside [0, E) -> zeros) fill with zeros.
+template <typename TI>
+__device__ __forceinline__ int route_expert(TI id, int num_experts, int drop_to) {
+  const int64_t e = (int64_t)id;
+  return (e >= 0 && e < num_experts) ? (int)e : drop_to;
+}
+
 template <typename TI>
 __global__ __launch_bounds__(256) void align_count(const TI* __restrict__ ids, int64_t n,
-                                                   int num_experts,
+                                                   int num_experts, int drop_to,
                                                    int32_t* __restrict__ counts) {
   __shared__ int hist[kMaxExperts];
   for (int e = threadIdx.x; e < num_experts; e += 256) hist[e] = 0;
@@ -50,8 +62,8 @@ __global__ __launch_bounds__(256) void align_count(const TI* __restrict__ ids, i
   for (int i = 0; i < kChunk / 256; ++i) {
     const int64_t r = base + i * 256 + threadIdx.x;
     if (r < n) {
-      const int64_t e = (int64_t)ids[r];
-      if (e >= 0 && e < num_experts) atomicAdd(&hist[e], 1);
+      const int e = route_expert(ids[r], num_experts, drop_to);
+      if (e >= 0) atomicAdd(&hist[e], 1);
     }
   }
   __syncthreads();
@@ -143,7 +155,7 @@ __global__ __launch_bounds__(1024) void align_scan(int32_t* __restrict__ counts,
 
 template <typename TI>
 __global__ __launch_bounds__(256) void align_place(const TI* __restrict__ ids, int64_t n,
-                                                   int num_experts, int id_bits,
+                                                   int num_experts, int drop_to, int id_bits,
                                                    const int32_t* __restrict__ starts,
                                                    int32_t* __restrict__ sorted_ids) {
   __shared__ int cursor[kMaxExperts];
@@ -160,10 +172,9 @@ __global__ __launch_bounds__(256) void align_place(const TI* __restrict__ ids, i
   const int64_t base = (int64_t)blockIdx.x * kChunk;
   for (int it = 0; it < kChunk / 256; ++it) {
     const int64_t r = base + it * 256 + tid;
-    int64_t e64 = -1;
-    if (r < n) e64 = (int64_t)ids[r];
-    const bool valid = e64 >= 0 && e64 < num_experts;
-    const int e = valid ? (int)e64 : 0;
+    const int em = r < n ? route_expert(ids[r], num_experts, drop_to) : -1;
+    const bool valid = em >= 0;
+    const int e = valid ? em : 0;
     uint64_t same = __ballot(valid);
     for (int bit = 0; bit < id_bits; ++bit) {
       const bool b = (e >> bit) & 1;
@@ -204,7 +215,8 @@ constexpr int kScanPlaceChunks = 64;
 
 template <typename TI>
 __global__ __launch_bounds__(512) void align_scan_place(const TI* __restrict__ ids, int64_t n,
-                                                        int num_experts, int id_bits, int block_m,
+                                                        int num_experts, int drop_to,
+                                                        int id_bits, int block_m,
                                                         const int32_t* __restrict__ counts,
                                                         int nchunks,
                                                         int32_t* __restrict__ sorted_ids,
@@ -226,9 +238,7 @@ __global__ __launch_bounds__(512) void align_scan_place(const TI* __restrict__ i
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int64_t r = rbase + j * 64 + lane;
-    int64_t e64 = -1;
-    if (r < n) e64 = (int64_t)ids[r];
-    eid[j] = (e64 >= 0 && e64 < ne) ? (int)e64 : -1;
+    eid[j] = r < n ? route_expert(ids[r], ne, drop_to) : -1;
   }
   const int ncnt = nchunks * ne;
   int cv[CB];
@@ -393,7 +403,8 @@ __global__ __launch_bounds__(256) void topk_sum(const T* __restrict__ d, const T
 // in-kernel time against per-chunk placement over the whole workgroup.
 template <typename TI, int NT, int RPT>
 __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, int64_t n,
-                                                   int num_experts, int id_bits, int block_m,
+                                                   int num_experts, int drop_to, int id_bits,
+                                                   int block_m,
                                                    int32_t* __restrict__ sorted_ids,
                                                    int32_t* __restrict__ expert_ids,
                                                    int32_t* __restrict__ num_post_padded) {
@@ -411,9 +422,7 @@ __global__ __launch_bounds__(NT) void align_single(const TI* __restrict__ ids, i
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int64_t r = rbase + j * 64 + lane;
-    int64_t e64 = -1;
-    if (r < n) e64 = (int64_t)ids[r];
-    eid[j] = (e64 >= 0 && e64 < num_experts) ? (int)e64 : -1;
+    eid[j] = r < n ? route_expert(ids[r], num_experts, drop_to) : -1;
   }
   for (int i = tid; i < W * E; i += NT) (&wpos[0][0])[i] = 0;
   __syncthreads();
@@ -538,31 +547,31 @@ int check_align_args(int64_t n, int num_experts, int block_m, int ids_dtype) {
 }
 
 template <typename TI>
-int launch_align(const TI* ids, int64_t n, int num_experts, int block_m, int32_t* sorted_ids,
-                 int32_t* expert_ids, int32_t* npp, int32_t* counts, int64_t nchunks,
-                 hipStream_t st) {
+int launch_align(const TI* ids, int64_t n, int num_experts, int drop_to, int block_m,
+                 int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, int32_t* counts,
+                 int64_t nchunks, hipStream_t st) {
   int id_bits = 0;
   while ((1 << id_bits) < num_experts) ++id_bits;
   const bool single = num_experts <= kSingleExperts;
   if (single && n <= kSingle) {
-    align_single<TI, 256, kSingle / 256><<<1, 256, 0, st>>>(ids, n, num_experts, id_bits, block_m,
-                                                            sorted_ids, expert_ids, npp);
+    align_single<TI, 256, kSingle / 256><<<1, 256, 0, st>>>(
+        ids, n, num_experts, drop_to, id_bits, block_m, sorted_ids, expert_ids, npp);
     return launch_status("align launch");
   }
   if (single && n <= kSingleWide) {
     align_single<TI, 1024, kSingleWide / 1024><<<1, 1024, 0, st>>>(
-        ids, n, num_experts, id_bits, block_m, sorted_ids, expert_ids, npp);
+        ids, n, num_experts, drop_to, id_bits, block_m, sorted_ids, expert_ids, npp);
     return launch_status("align launch");
   }
   if (nchunks > 0) {
-    align_count<TI><<<(unsigned)nchunks, 256, 0, st>>>(ids, n, num_experts, counts);
+    align_count<TI><<<(unsigned)nchunks, 256, 0, st>>>(ids, n, num_experts, drop_to, counts);
     int rc = launch_status("align count launch");
     if (rc) return rc;
   }
   if (nchunks > 0 && nchunks <= kScanPlaceChunks) {
-    align_scan_place<TI><<<(unsigned)nchunks, 512, 0, st>>>(ids, n, num_experts, id_bits, block_m,
-                                                             counts, (int)nchunks, sorted_ids,
-                                                             expert_ids, npp);
+    align_scan_place<TI><<<(unsigned)nchunks, 512, 0, st>>>(ids, n, num_experts, drop_to, id_bits,
+                                                             block_m, counts, (int)nchunks,
+                                                             sorted_ids, expert_ids, npp);
     return launch_status("align scan+place launch");
   }
   align_scan<<<1, kMaxExperts, 0, st>>>(counts, (int)nchunks, num_experts, block_m, n, sorted_ids,
@@ -570,21 +579,23 @@ int launch_align(const TI* ids, int64_t n, int num_experts, int block_m, int32_t
   int rc = launch_status("align scan launch");
   if (rc) return rc;
   if (nchunks > 0) {
-    align_place<TI><<<(unsigned)nchunks, 256, 0, st>>>(ids, n, num_experts, id_bits, counts,
-                                                       sorted_ids);
+    align_place<TI><<<(unsigned)nchunks, 256, 0, st>>>(ids, n, num_experts, drop_to, id_bits,
+                                                       counts, sorted_ids);
     rc = launch_status("align place launch");
   }
   return rc;
 }
 
+// drop_to: -1 (routes of ids outside [0, num_experts) are dropped) or
+// num_experts - 1 (they gather in that last expert's blocks).
 int do_align(const void* ids, int ids_dtype, int64_t n, int num_experts, int block_m,
              int32_t* sorted_ids, int32_t* expert_ids, int32_t* npp, int32_t* counts,
-             int64_t nchunks, hipStream_t st) {
+             int64_t nchunks, hipStream_t st, int drop_to = -1) {
   if (ids_dtype == MXFP4_DT_I32)
-    return launch_align(static_cast<const int32_t*>(ids), n, num_experts, block_m, sorted_ids,
-                        expert_ids, npp, counts, nchunks, st);
-  return launch_align(static_cast<const int64_t*>(ids), n, num_experts, block_m, sorted_ids,
-                      expert_ids, npp, counts, nchunks, st);
+    return launch_align(static_cast<const int32_t*>(ids), n, num_experts, drop_to, block_m,
+                        sorted_ids, expert_ids, npp, counts, nchunks, st);
+  return launch_align(static_cast<const int64_t*>(ids), n, num_experts, drop_to, block_m,
+                      sorted_ids, expert_ids, npp, counts, nchunks, st);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -687,14 +698,14 @@ extern "C" int mxfp4_moe_align(const void* topk_ids, int ids_dtype, int64_t num_
                   static_cast<hipStream_t>(stream));
 }
 
-extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
-                              const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,
-                              int64_t num_experts, int64_t n, int64_t k, void* c, int c_dtype,
-                              int64_t c_row_stride, const float* a_scale, const float* b_scale,
-                              const float* topk_weights, int mul_routed_weight,
-                              const int32_t* sorted_ids, const int32_t* expert_ids,
-                              const int32_t* num_post_padded, int64_t em, int block_m,
-                              int64_t num_valid, int top_k, void* stream) {
+namespace mx {
+namespace {
+
+// Checks shared by the routed GEMM entry points (mxfp4_moe_gemm,
+// mxfp4_fused_moe); em / block_m are the metadata capacity and block size.
+int check_routed_args(const void* a, int a_dtype, int64_t a_row_stride, const uint8_t* a_mx,
+                      const uint8_t* b, int64_t num_experts, int64_t n, int64_t k, int c_dtype,
+                      int top_k, int block_m, int64_t em) {
   if (c_dtype != MXFP4_DT_BF16 && c_dtype != MXFP4_DT_F16 && c_dtype != MXFP4_DT_F32) {
     set_error("unsupported software fallback compute dtype: %d", c_dtype);
     return MXFP4_ERR_TYPE;
@@ -714,7 +725,16 @@ extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_
     set_error("moe gemm: activation/weight rows must be 16-byte aligned");
     return MXFP4_ERR_VALUE;
   }
-  if (em == 0) return MXFP4_OK;
+  return MXFP4_OK;
+}
+
+GemmArgs routed_args(const void* a, int64_t a_rows, int64_t a_row_stride, const uint8_t* a_mx,
+                     const uint8_t* b, const uint8_t* b_mx, int64_t num_experts, int64_t n,
+                     int64_t k, void* c, int64_t c_row_stride, const float* a_scale,
+                     const float* b_scale, const float* topk_weights, int mul_routed_weight,
+                     const int32_t* sorted_ids, const int32_t* expert_ids,
+                     const int32_t* num_post_padded, int64_t em, int block_m, int64_t num_valid,
+                     int top_k) {
   GemmArgs g = {};
   g.a = a;
   g.a_mx = a_mx;
@@ -742,7 +762,152 @@ extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_
   g.top_k = top_k;
   g.block_m = block_m;
   g.num_experts = (int32_t)num_experts;
+  return g;
+}
+
+// Rows per expert block of the fused soft op.  Its weights come in the
+// checkpoint layout, where a prefill tile stages 32 bytes of every weight
+// row per 64-deep step (one cache line per row), so blocks of more rows
+// amortize the weight loads better than on the prepacked layout.  W4A16,
+// E=128, top-8, routed GEMM alone, graph replays (MI355X; K=2048 N=1536 /
+// K=768 N=2048 per routes per expert): 16 -> 32-row blocks 51.6 / 28.4 us
+// (64 rows: 54.6 / 33.2); 32 -> 64 rows 59.0 / 35.9 (32 rows: 67.7 /
+// 35.1); 48 -> 64 rows 66.2 / 41.3 (128: 76.5 / 47.1); 64 -> 128 rows
+// 80.2 / 52.3 (64: 84.0 / 49.3); 256 -> 128 rows 235.9 / 146.5 (64: 235.8 /
+// 151.0).  The W4A4 and FP32 paths keep the 16 / 32 / 64 rule.
+int soft_block_m(int64_t routes, int64_t num_experts, bool w4a16) {
+  const double avg = (double)routes / (double)(num_experts > 0 ? num_experts : 1);
+  if (avg <= 1.5) return 16;
+  if (!w4a16) return avg <= 32.0 ? 32 : 64;
+  return avg <= 28.0 ? 32 : (avg <= 56.0 ? 64 : 128);
+}
+
+struct SoftPlan {
+  int block_m;
+  int align_experts;  // experts the routing counts (E + 1: dropped routes in the last)
+  int drop_to;        // route_expert's target for ids outside [0, E)
+  bool zero_c;        // E + 1 experts do not fit the routing: zero C first instead
+  int64_t max_sorted, max_blocks, nchunks;
+  int64_t off_counts, off_sorted, off_experts, off_npp, total;
+};
+
+SoftPlan plan_soft(int64_t routes, int64_t num_experts, bool w4a16) {
+  SoftPlan p;
+  p.block_m = soft_block_m(routes, num_experts, w4a16);
+  p.zero_c = num_experts + 1 > kMaxExperts;
+  p.align_experts = (int)(p.zero_c ? num_experts : num_experts + 1);
+  p.drop_to = p.zero_c ? -1 : (int)num_experts;
+  align_capacity(routes, p.align_experts, p.block_m, &p.max_sorted, &p.max_blocks, &p.nchunks);
+  int64_t off = 0;
+  p.off_counts = off;
+  off = round_up(off + (p.nchunks > 0 ? p.nchunks : 1) * p.align_experts * 4, 256);
+  p.off_sorted = off; off = round_up(off + p.max_sorted * 4, 256);
+  p.off_experts = off; off = round_up(off + p.max_blocks * 4, 256);
+  p.off_npp = off; off = round_up(off + 4, 256);
+  p.total = off;
+  return p;
+}
+
+// Zero `bytes` bytes at p (16-byte aligned; bytes % 2 == 0): a fill kernel,
+// not hipMemsetAsync, so the call can be captured in a graph.
+__global__ __launch_bounds__(256) void zero_fill(uint8_t* __restrict__ p, int64_t bytes) {
+  const int64_t nv = bytes / 16;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < nv; i += stride)
+    reinterpret_cast<i32x4*>(p)[i] = i32x4{0, 0, 0, 0};
+  for (int64_t i = nv * 16 + blockIdx.x * 256 + threadIdx.x; i < bytes; i += stride) p[i] = 0;
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
+                              const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,
+                              int64_t num_experts, int64_t n, int64_t k, void* c, int c_dtype,
+                              int64_t c_row_stride, const float* a_scale, const float* b_scale,
+                              const float* topk_weights, int mul_routed_weight,
+                              const int32_t* sorted_ids, const int32_t* expert_ids,
+                              const int32_t* num_post_padded, int64_t em, int block_m,
+                              int64_t num_valid, int top_k, void* stream) {
+  int rc = check_routed_args(a, a_dtype, a_row_stride, a_mx, b, num_experts, n, k, c_dtype, top_k,
+                             block_m, em);
+  if (rc) return rc;
+  if (em == 0) return MXFP4_OK;
+  const GemmArgs g = routed_args(a, a_rows, a_row_stride, a_mx, b, b_mx, num_experts, n, k, c,
+                                 c_row_stride, a_scale, b_scale, topk_weights, mul_routed_weight,
+                                 sorted_ids, expert_ids, num_post_padded, em, block_m, num_valid,
+                                 top_k);
   return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mxfp4_fused_moe_workspace_size(int64_t m, int top_k, int64_t num_experts,
+                                              int a_dtype, int c_dtype, int64_t* bytes) {
+  if (bytes == nullptr || m < 0 || top_k < 1 || num_experts < 1 || num_experts > kMaxExperts ||
+      m * top_k > (int64_t)0x3FFFFFFF) {
+    set_error("fused moe: invalid sizes (m %lld, top_k %d, experts %lld)", (long long)m, top_k,
+              (long long)num_experts);
+    return MXFP4_ERR_VALUE;
+  }
+  const bool w4a16 = a_dtype != MXFP4_DT_U8 && c_dtype != MXFP4_DT_F32;
+  *bytes = plan_soft(m * top_k, num_experts, w4a16).total;
+  return MXFP4_OK;
+}
+
+extern "C" int mxfp4_fused_moe(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
+                               const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,
+                               int64_t num_experts, int64_t n, int64_t k, void* c, int c_dtype,
+                               const float* a_scale, const float* b_scale,
+                               const float* topk_weights, int mul_routed_weight,
+                               const void* topk_ids, int ids_dtype, int64_t m, int top_k,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
+  if (ids_dtype != MXFP4_DT_I32 && ids_dtype != MXFP4_DT_I64) {
+    set_error("topk_ids must be int32 or int64");
+    return MXFP4_ERR_TYPE;
+  }
+  if (m < 0 || m * (int64_t)(top_k > 0 ? top_k : 1) > (int64_t)0x3FFFFFFF ||
+      num_experts > kMaxExperts) {
+    set_error("fused moe: invalid sizes (m %lld, top_k %d, experts %lld)", (long long)m, top_k,
+              (long long)num_experts);
+    return MXFP4_ERR_VALUE;
+  }
+  const int64_t routes = m * top_k;
+  const bool w4a16 = a_dtype != MXFP4_DT_U8 && c_dtype != MXFP4_DT_F32;
+  const SoftPlan p = plan_soft(routes, num_experts, w4a16);
+  int rc = check_routed_args(a, a_dtype, a_row_stride, a_mx, b, num_experts, n, k, c_dtype, top_k,
+                             p.block_m, p.max_sorted);
+  if (rc) return rc;
+  if (!aligned16(c)) {
+    set_error("fused moe: C must be 16-byte aligned");
+    return MXFP4_ERR_VALUE;
+  }
+  if (workspace_bytes < p.total || (p.total > 0 && !aligned16(workspace))) {
+    set_error("fused moe: workspace too small or misaligned (%lld < %lld bytes)",
+              (long long)workspace_bytes, (long long)p.total);
+    return MXFP4_ERR_VALUE;
+  }
+  if (routes == 0) return MXFP4_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + p.off_counts);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws + p.off_sorted);
+  int32_t* experts = reinterpret_cast<int32_t*>(ws + p.off_experts);
+  int32_t* npp = reinterpret_cast<int32_t*>(ws + p.off_npp);
+  if (p.zero_c) {
+    const int64_t bytes = routes * n * elem_size(c_dtype);
+    const int64_t blocks = std::min<int64_t>((bytes / 16 + 255) / 256 + 1, 4096);
+    zero_fill<<<(unsigned)blocks, 256, 0, st>>>(static_cast<uint8_t*>(c), bytes);
+    rc = launch_status("fused moe zero fill launch");
+    if (rc) return rc;
+  }
+  rc = do_align(topk_ids, ids_dtype, routes, p.align_experts, p.block_m, sorted, experts, npp,
+                counts, p.nchunks, st, p.drop_to);
+  if (rc) return rc;
+  const GemmArgs g = routed_args(a, a_rows, a_row_stride, a_mx, b, b_mx, num_experts, n, k, c, n,
+                                 a_scale, b_scale, topk_weights, mul_routed_weight, sorted, experts,
+                                 npp, p.max_sorted, p.block_m, routes, top_k);
+  return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, st);
 }
 
 extern "C" int mxfp4_linear_w4a16_workspace_size(int64_t m, int64_t k, int64_t n, int64_t* bytes) {

@@ -75,18 +75,6 @@ def _is_validated_triton_linear_shape(m: int, n: int) -> bool:
     return m >= 370 and n >= 2048
 
 
-def _routing_block_m(num_routes: int, num_experts: int) -> int:
-    """Rows per expert block for the routed GEMMs, from the mean rows per
-    expert (the MoE layer's rule: 32-row blocks run 32 x 256 tiles and win
-    from ~1.5 rows per expert, 64-row ones, on 64 x 256 tiles, from ~32)."""
-    avg = num_routes / max(num_experts, 1)
-    if avg <= 1.5:
-        return 16
-    if avg <= 32:
-        return 32
-    return 64
-
-
 def dequant_mxfp4(
     packed: torch.Tensor,
     block_scales: torch.Tensor,
@@ -337,11 +325,16 @@ def fused_moe_mxfp4_soft(
     rounding to C.dtype.  A is bf16/fp16/fp32 (converted to C.dtype, soft:475)
     or packed MXFP4 with ``A_mx_scale`` (W4A4 on the block-scaled MFMA).
     Like the reference's safe path, the routing metadata arguments are not
-    consulted (soft:466): routing is rebuilt on the device from ``topk_ids``
-    with no host synchronisation.  With ``MXFP4_GFX936_BACKEND=triton`` the
-    reference's checks of that backend run first (soft:410-427: compiler,
-    unpacked activations, non-empty metadata of a supported block size, K a
-    multiple of 128; RuntimeError otherwise); the result is the same one.
+    consulted (soft:466): one library call builds the routing on the device
+    from ``topk_ids`` (no host synchronisation) and runs the grouped GEMM;
+    rows of out-of-range ids get zeros, so C needs no separate fill.  With
+    ``MXFP4_GFX936_BACKEND=triton`` the reference's checks of that backend
+    run (soft:410-427: compiler, unpacked activations, non-empty metadata of
+    a supported block size, K a multiple of 128; RuntimeError otherwise) and,
+    as its Triton kernel does (soft:428-464, 100-115), C is zero-filled and
+    the grouped GEMM runs over the caller's ``sorted_token_ids`` /
+    ``expert_ids`` / ``num_tokens_post_padded`` (expert -1 blocks give
+    zeros; routes the metadata does not name stay zero).
     """
     if swizzle_mx_a or swizzle_mx_b:
         raise NotImplementedError("the gfx936 software fallback does not support swizzled scales")
@@ -372,23 +365,77 @@ def fused_moe_mxfp4_soft(
         block_m = sorted_token_ids.numel() // expert_ids.numel()
         if block_m not in (16, 32, 64, 128):
             raise RuntimeError(f"unsupported Triton routing block size: {block_m}")
+        _fused_moe_caller_metadata(A, B, C, A_scale, B_scale, B_mx_scale, topk_weights, topk_ids,
+                                   sorted_token_ids, expert_ids, num_tokens_post_padded,
+                                   mul_routed_weight, top_k, block_m)
+        return
     del sorted_token_ids, expert_ids, num_tokens_post_padded
     # operand checks first (soft:468-477), then the device
     act, act_mx, b, b_mx, a_scale, b_scale, weights, ids = _prepare_moe_operands(
         A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights, topk_ids, top_k)
     device = _lib.require_device(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale,
                                  topk_weights, topk_ids)
+    m = ids.shape[0]
+    num_routes = ids.numel()
+    if num_routes == 0 or C.numel() == 0:
+        return
+    lib = _lib.load()
+    num_experts, n, k = b.shape[0], b.shape[1], b.shape[2] * 2
+    a_code, c_code = _lib.dtype_code(act.dtype), _lib.dtype_code(C.dtype)
+    ws_bytes = _fused_workspace_bytes(lib, m, top_k, num_experts, a_code, c_code)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    out = C if C.is_contiguous() and C.data_ptr() % 16 == 0 else torch.empty(
+        C.shape, dtype=C.dtype, device=device)
+    with _lib.on_device(device):
+        _lib.check(lib.mxfp4_fused_moe(
+            _lib.ptr(act), a_code, act.shape[0], act.stride(0), _lib.ptr(act_mx), _lib.ptr(b),
+            _lib.ptr(b_mx), num_experts, n, k, _lib.ptr(out), c_code, _lib.ptr(a_scale),
+            _lib.ptr(b_scale), _lib.ptr(weights), 1 if mul_routed_weight else 0, _lib.ptr(ids),
+            _lib.dtype_code(ids.dtype), m, top_k, _lib.ptr(ws), ws_bytes,
+            _lib.stream_of(device)))
+    if out is not C:
+        C.copy_(out)
 
+
+_FUSED_WS: dict = {}
+
+
+def _fused_workspace_bytes(lib, m: int, top_k: int, num_experts: int, a_code: int,
+                           c_code: int) -> int:
+    """Workspace bytes of mxfp4_fused_moe (a pure function of the sizes, cached)."""
+    key = (m, top_k, num_experts, a_code, c_code)
+    v = _FUSED_WS.get(key)
+    if v is None:
+        out = ctypes.c_int64(0)
+        _lib.check(lib.mxfp4_fused_moe_workspace_size(m, top_k, num_experts, a_code, c_code,
+                                                      ctypes.byref(out)))
+        if len(_FUSED_WS) >= 4096:
+            _FUSED_WS.clear()
+        v = _FUSED_WS[key] = out.value
+    return v
+
+
+def _fused_moe_caller_metadata(A, B, C, A_scale, B_scale, B_mx_scale, topk_weights, topk_ids,
+                               sorted_token_ids, expert_ids, num_tokens_post_padded,
+                               mul_routed_weight, top_k, block_m):
+    """The ``triton`` backend value (soft:428-464): C zero-filled, then the
+    grouped GEMM over the caller's routing metadata (its kernel takes no
+    A_mx_scale: the activations are unpacked)."""
+    act, act_mx, b, b_mx, a_scale, b_scale, weights, ids = _prepare_moe_operands(
+        A, B, C, A_scale, B_scale, None, B_mx_scale, topk_weights, topk_ids, top_k)
+    device = _lib.require_device(A, B, C, A_scale, B_scale, B_mx_scale, topk_weights, topk_ids,
+                                 sorted_token_ids, expert_ids, num_tokens_post_padded)
     C.zero_()
     num_routes = ids.numel()
     if num_routes == 0 or C.numel() == 0:
         return
-    block_m = _routing_block_m(num_routes, B.shape[0])
-    sorted_ids, expert_blk, npp = make_routing_device(ids, B.shape[0], block_m)
+    sorted_ids = sorted_token_ids.to(torch.int32).contiguous()
+    experts = expert_ids.to(torch.int32).contiguous()
+    npp = num_tokens_post_padded.reshape(1).to(torch.int32).contiguous()
     out = C if C.is_contiguous() and C.data_ptr() % 16 == 0 else torch.zeros(
         C.shape, dtype=C.dtype, device=device)
     _moe_gemm_launch(act, act_mx, b, b_mx, out.view(num_routes, B.shape[1]), a_scale, b_scale,
-                     weights, mul_routed_weight, sorted_ids, expert_blk, npp, block_m, num_routes,
+                     weights, mul_routed_weight, sorted_ids, experts, npp, block_m, num_routes,
                      top_k, device)
     if out is not C:
         C.copy_(out)

@@ -1,0 +1,180 @@
+"""GPU parity: ``fused_moe_mxfp4_soft`` through its one library call
+(``mxfp4_fused_moe``: device routing + the grouped GEMM, soft:379-494).
+
+The safe path zero-fills C and then writes the rows of routes whose expert id
+is in range (soft:476-494).  The library writes zeros only to the rows no GEMM
+row covers (the routing gathers out-of-range ids in blocks of an extra
+expert, which the GEMMs fill with zeros), so every test starts from a C full
+of NaN: any row left unwritten fails.  The sizes pick each routing block
+size (16 / 32 / 64 / 128 rows, from the routes per expert) and each compute
+path (W4A16 bf16 / fp16, packed-A W4A4, C in FP32)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mxfp4_amd as mx
+from oracle import mxfp4_oracle as O
+
+from _helpers import assert_parity, cuda, rand_act, rand_mxfp4
+
+pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::RuntimeWarning")]
+
+
+def _empty():
+    return torch.empty(0, device="cuda")
+
+
+def _route_with_dropped(m, e, top_k, seed, dropped):
+    """softmax -> top-k of seeded logits; then `dropped` of the slots get ids
+    outside [0, e) (-1, e, e + 7 in turn)."""
+    g = torch.Generator().manual_seed(seed)
+    w, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
+    ids = ids.clone()
+    if dropped:
+        pick = torch.randperm(m * top_k, generator=g)[:dropped]
+        bad = torch.tensor([-1, e, e + 7])[torch.arange(dropped) % 3]
+        ids.view(-1)[pick] = bad
+    return w.float(), ids
+
+
+def _run(a, a_mx, wp, ws, ids, w, c_dtype, mul, a_scale=0.75, b_scale=None):
+    m, top_k = ids.shape
+    e, n = wp.shape[0], wp.shape[1]
+    bs = torch.ones(e) if b_scale is None else b_scale
+    C = torch.full((m, top_k, n), float("nan"), dtype=c_dtype, device="cuda")
+    mx.fused_moe_mxfp4_soft(cuda(a), cuda(wp), C, torch.full((1,), a_scale, device="cuda"),
+                            cuda(bs), None if a_mx is None else cuda(a_mx), cuda(ws), cuda(w),
+                            cuda(ids), _empty(), _empty(), _empty(), mul, top_k, False, False)
+    return C
+
+
+# (tokens, experts, top_k) -> routes per expert 1 / 16 / 40 / 128: routing
+# blocks of 16 / 32 / 64 / 128 rows
+BLOCK_CASES = [(8, 64, 8), (64, 16, 4), (160, 16, 4), (512, 16, 4)]
+
+
+@pytest.mark.parametrize("m,e,top_k", BLOCK_CASES, ids=["blk16", "blk32", "blk64", "blk128"])
+@pytest.mark.parametrize("c_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("dropped", [0, 37], ids=["all_valid", "dropped"])
+def test_soft_op_every_row_written(m, e, top_k, c_dtype, dropped):
+    rng = np.random.default_rng(m + e)
+    k, n = 256, 192  # a ragged last column tile for the 128- and 256-wide tiles
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(m + 3, (m, k))
+    w, ids = _route_with_dropped(m, e, top_k, 1000 + m, min(dropped, m * top_k // 2))
+    b_scale = torch.linspace(0.5, 1.5, e)
+    C = _run(a, None, wp, ws, ids, w, c_dtype, True, b_scale=b_scale)
+    out = C.float().cpu().numpy()
+    assert not np.isnan(out).any(), "a row of C was left unwritten"
+    ids_np = ids.numpy()
+    bad = (ids_np < 0) | (ids_np >= e)
+    assert np.all(out[bad] == 0), "rows of out-of-range ids must be zero (soft:476)"
+    dt = "f16" if c_dtype == torch.float16 else "bf16"
+    oracle = O.fused_moe_fp64(O.round_to_dtype(a.float().numpy(), dt), wp, ws, 0.75,
+                              b_scale.numpy(), w.numpy(), ids_np, True, compute_dtype=dt)
+    assert_parity(out, oracle, what=f"m={m} e={e} top_k={top_k} {dt} dropped={int(bad.sum())}")
+
+
+@pytest.mark.parametrize("m,e,top_k", [(64, 16, 4), (512, 16, 4)], ids=["blk32", "blk64"])
+def test_soft_op_w4a4_every_row_written(m, e, top_k):
+    rng = np.random.default_rng(7 * m)
+    k, n = 512, 160
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    ap, asc = O.quant_mxfp4_rne(rand_act(m + 5, (m, k)).float().numpy())
+    w, ids = _route_with_dropped(m, e, top_k, 2000 + m, 23)
+    C = _run(ap, asc, wp, ws, ids, w, torch.bfloat16, False)
+    out = C.float().cpu().numpy()
+    assert not np.isnan(out).any(), "a row of C was left unwritten"
+    ids_np = ids.numpy()
+    assert np.all(out[(ids_np < 0) | (ids_np >= e)] == 0)
+    oracle = O.fused_moe_fp64(O.dequant_values(ap, asc, "bf16"), wp, ws, 0.75, np.ones(e),
+                              w.numpy(), ids_np, False)
+    assert_parity(out, oracle, what=f"w4a4 m={m}")
+
+
+@pytest.mark.parametrize("m,e,top_k", [(8, 64, 8), (160, 16, 4)], ids=["blk16", "blk64"])
+def test_soft_op_fp32_every_row_written(m, e, top_k):
+    rng = np.random.default_rng(11 * m)
+    k, n = 256, 96
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(m + 9, (m, k)).float()
+    w, ids = _route_with_dropped(m, e, top_k, 3000 + m, 19)
+    C = _run(a, None, wp, ws, ids, w, torch.float32, True)
+    out = C.cpu().numpy()
+    assert not np.isnan(out).any(), "a row of C was left unwritten"
+    ids_np = ids.numpy()
+    assert np.all(out[(ids_np < 0) | (ids_np >= e)] == 0)
+    oracle = O.fused_moe_fp64(a.numpy(), wp, ws, 0.75, np.ones(e), w.numpy(), ids_np, True,
+                              compute_dtype="f32")
+    assert_parity(out, oracle, what=f"fp32 m={m}")
+
+
+def test_soft_op_1024_experts_zero_fill():
+    # 1024 experts leave no room for the extra expert of dropped routes: the
+    # call zero-fills C with a fill kernel and routes the valid ids only
+    rng = np.random.default_rng(1024)
+    m, e, top_k, k, n = 96, 1024, 4, 128, 48
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(1025, (m, k))
+    w, ids = _route_with_dropped(m, e, top_k, 1026, 31)
+    C = _run(a, None, wp, ws, ids, w, torch.bfloat16, True)
+    out = C.float().cpu().numpy()
+    assert not np.isnan(out).any()
+    ids_np = ids.numpy()
+    assert np.all(out[(ids_np < 0) | (ids_np >= e)] == 0)
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 0.75, np.ones(e), w.numpy(), ids_np,
+                              True)
+    assert_parity(out, oracle, what="1024 experts")
+
+
+def test_soft_op_gate_up_shape_512_tokens():
+    # BASELINE config 3's gate_up at 512 tokens (the bench row): 64-row
+    # blocks on 64 x 128 tiles of the checkpoint layout; sampled rows vs the
+    # FP64 oracle, every row written
+    rng = np.random.default_rng(20260818)
+    m, e, top_k, k, n = 512, 128, 8, 2048, 1536
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(20260819, (m, k))
+    w, ids = _route_with_dropped(m, e, top_k, 20260820, 0)
+    C = _run(a, None, wp, ws, ids, w, torch.bfloat16, True, a_scale=1.0)
+    out = C.float().cpu().numpy()
+    assert not np.isnan(out).any()
+    rows = np.arange(0, m, 37)
+    oracle = O.fused_moe_fp64(a.float().numpy()[rows], wp, ws, 1.0, np.ones(e),
+                              w.numpy()[rows], ids.numpy()[rows], True)
+    assert_parity(out[rows], oracle, what="gate_up 512 tokens")
+
+
+@pytest.mark.parametrize("block_m", [16, 32, 64, 128])
+def test_soft_op_triton_backend_uses_caller_metadata(block_m, monkeypatch):
+    # MXFP4_GFX936_BACKEND=triton (soft:409-464): C zero-filled, then the
+    # grouped GEMM over the caller's metadata; an expert -1 block writes
+    # zeros and routes the metadata leaves out stay zero
+    rng = np.random.default_rng(block_m + 50)
+    m, k, n, e, top_k = 40, 256, 96, 5, 2
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(block_m + 51, (m, k))
+    w, ids = _route_with_dropped(m, e, top_k, 500 + block_m, 0)
+    ids_np = ids.numpy()
+    srt, exp_, npp = O.make_routing(ids_np, block_m=block_m, num_experts=e)
+    srt, exp_ = srt.copy(), exp_.copy()
+    exp_[exp_ == 2] = -1                            # not on this device
+    left_out = srt[(srt < m * top_k)][:3].copy()    # three routes the metadata omits
+    srt[np.isin(srt, left_out)] = m * top_k
+    monkeypatch.setenv("MXFP4_GFX936_BACKEND", "triton")
+    C = torch.full((m, top_k, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4_soft(cuda(a), cuda(wp), C, torch.tensor([0.5], device="cuda"),
+                            torch.linspace(1, 2, e, device="cuda"), None, cuda(ws), cuda(w),
+                            cuda(ids), cuda(srt), cuda(exp_), cuda(npp), True, top_k, False,
+                            False)
+    out = C.float().cpu().numpy()
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 0.5, np.linspace(1, 2, e), w.numpy(),
+                              ids_np, True)
+    oracle[ids_np == 2] = 0.0
+    oracle.reshape(m * top_k, n)[left_out] = 0.0
+    assert not np.isnan(out).any()
+    assert np.all(out.reshape(m * top_k, n)[left_out] == 0)
+    assert_parity(out, oracle, what=f"triton backend block {block_m}")
