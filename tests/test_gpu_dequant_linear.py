@@ -65,6 +65,56 @@ def test_dequant_expert_shapes_vs_c_oracle(dt):
     assert np.array_equal(_bits(out, dt), c_oracle.dequant_bits(packed, scales, dt))
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,k", [(300, 2080), (5000, 96), (7, 4096 + 64)])
+def test_dequant_ragged_blocks_vs_c_oracle(rows, k, dt):
+    # 16-byte rows go through the wide kernel, whose waves take 2048-value
+    # blocks: a last block of one chunk (K = 2080), rows shorter than a block
+    # (K = 96) over a grid-stride loop, and a ragged tail after two blocks
+    rng = np.random.default_rng(rows + k)
+    packed, scales = rand_mxfp4(rng, (rows,), k, lo=0, hi=255)
+    out = mx.dequant_mxfp4(cuda(packed), cuda(scales), TDT[dt])
+    assert np.array_equal(_bits(out, dt), c_oracle.dequant_bits(packed, scales, dt))
+
+
+@pytest.mark.parametrize("dt,rows", [("bf16", 65536), ("f32", 32768)])
+def test_dequant_streaming_output_sampled_rows(dt, rows):
+    # outputs of >= 256 MiB are written with non-temporal stores; sampled
+    # rows (and the last) bit-exact against the C oracle
+    rng = np.random.default_rng(rows)
+    k = 2048
+    packed = torch.randint(0, 256, (rows, k // 2), dtype=torch.uint8, device="cuda")
+    scales = torch.randint(0, 256, (rows, k // 32), dtype=torch.uint8, device="cuda")
+    out = mx.dequant_mxfp4(packed, scales, TDT[dt])
+    assert out.numel() * out.element_size() >= 256 << 20
+    pick = torch.from_numpy(np.sort(np.append(rng.choice(rows, 256, replace=False), rows - 1)))
+    got = _bits(out[pick.cuda()], dt)
+    want = c_oracle.dequant_bits(packed[pick.cuda()].cpu().numpy(),
+                                 scales[pick.cuda()].cpu().numpy(), dt)
+    del out
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_dequant_c_abi_four_byte_row_stride(dt):
+    # a packed row stride that is 4-byte but not 16-byte aligned takes the
+    # dword kernel (the C ABI accepts any multiple of 4)
+    rng = np.random.default_rng(99)
+    rows, k = 37, 160
+    packed, scales = rand_mxfp4(rng, (rows,), k, lo=0, hi=255)
+    stride = k // 2 + 4
+    buf = np.zeros((rows, stride), dtype=np.uint8)
+    buf[:, : k // 2] = packed
+    p, s = cuda(buf), cuda(scales)
+    out = torch.empty((rows, k), dtype=TDT[dt], device="cuda")
+    lib = _lib.load()
+    rc = lib.mxfp4_dequant(p.data_ptr(), stride, s.data_ptr(), k // 32, rows, k, out.data_ptr(),
+                           _lib.dtype_code(TDT[dt]),
+                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, lib.mxfp4_last_error()
+    assert np.array_equal(_bits(out, dt), c_oracle.dequant_bits(packed, scales, dt))
+
+
 def test_dequant_noncontiguous_and_other_dtype():
     rng = np.random.default_rng(7)
     packed, scales = rand_mxfp4(rng, (64,), 256)
