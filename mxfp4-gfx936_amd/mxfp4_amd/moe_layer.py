@@ -78,8 +78,10 @@ def moe_layer(
     top_k = topk_ids.shape[1]
     device = _lib.require_device(x, w13, w13_scale, w2, w2_scale, topk_weights, topk_ids)
     lib = _lib.load()
-    pre13 = check_prepacked(prepacked13, num_experts, 2 * inter, hidden, device, "moe_layer w13")
-    pre2 = check_prepacked(prepacked2, num_experts, hidden, inter, device, "moe_layer w2")
+    pre13 = check_prepacked(prepacked13, num_experts, 2 * inter, hidden, device,
+                            "moe_layer w13", w13, w13_scale)
+    pre2 = check_prepacked(prepacked2, num_experts, hidden, inter, device, "moe_layer w2", w2,
+                           w2_scale)
 
     xc = _lib.aligned(x)
     ids = topk_ids if topk_ids.dtype in (torch.int32, torch.int64) else topk_ids.to(torch.int64)

@@ -171,7 +171,8 @@ def linear_mxfp4_soft(
     device = _lib.require_device(x, packed, block_scales, bias)
     lib = _lib.load()
     n = packed.shape[0]
-    pre = check_prepacked(prepacked, 1, n, logical_k, device, "linear_mxfp4_soft")
+    pre = check_prepacked(prepacked, 1, n, logical_k, device, "linear_mxfp4_soft", packed,
+                          block_scales)
     x_2d = _lib.aligned(x.reshape(-1, logical_k))
     w = _lib.aligned(packed)
     s = block_scales.contiguous()

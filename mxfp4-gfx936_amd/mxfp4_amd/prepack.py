@@ -15,8 +15,15 @@ their prefill kernels; the results are bitwise equal to the checkpoint-layout
 calls.  Decode-sized calls keep using the checkpoint layout, which must stay
 allocated.
 
-A copy belongs to the weights it was made from: after they change, prepack
-again (``PrepackedWeights.matches`` checks shapes and device, not contents).
+A copy belongs to the weights it was made from.  It records their storage
+address and version counter (``Tensor._version``, which in-place writes to
+the tensor or its views bump); a call given the copy with other tensors, or
+with the same tensors after such a write (``with torch.no_grad():
+param.copy_(...)``), raises ``ValueError`` instead of reading stale
+weights, and the vLLM hooks prepack such weights again before the call.
+Writes through ``param.data`` are not versioned by PyTorch (``.data`` is a
+new tensor with its own counter) and are not seen: prepack again after them
+(``vllm_adapter.refresh_prepacked(layer)`` for a vLLM layer).
 """
 
 from __future__ import annotations
@@ -42,10 +49,30 @@ class PrepackedWeights:
     experts: int
     rows: int
     k: int
+    # (data_ptr, _version) of the packed weights and of the scales it was
+    # made from; None when unknown (a copy built by hand)
+    source: tuple | None = None
 
     def matches(self, experts: int, rows: int, k: int, device: torch.device) -> bool:
         return (self.experts, self.rows, self.k) == (experts, rows, k) and \
             self.nibbles.device == device and self.scales.device == device
+
+    def is_current(self, packed: torch.Tensor, block_scales: torch.Tensor) -> bool:
+        """True when (packed, block_scales) are the tensors this copy was made
+        from and neither was written in place since."""
+        if self.source is None:
+            return True
+        return self.source == (_source_of(packed), _source_of(block_scales))
+
+
+def _source_of(t: torch.Tensor):
+    """(storage address, version counter) of a tensor; inference-mode tensors
+    keep no version counter, and then only the address is compared."""
+    try:
+        version = t._version
+    except RuntimeError:
+        version = None
+    return (t.data_ptr(), version)
 
 
 def prepack_w4a16(packed: torch.Tensor, block_scales: torch.Tensor) -> PrepackedWeights:
@@ -77,12 +104,16 @@ def prepack_w4a16(packed: torch.Tensor, block_scales: torch.Tensor) -> Prepacked
         _lib.check(lib.mxfp4_prepack_w4a16(
             _lib.ptr(w), _lib.ptr(s), experts, rows, k, _lib.ptr(nibbles), _lib.ptr(scales),
             _lib.stream_of(device)))
-    return PrepackedWeights(nibbles, scales, experts, rows, k)
+    return PrepackedWeights(nibbles, scales, experts, rows, k,
+                            (_source_of(packed), _source_of(block_scales)))
 
 
 def check_prepacked(pre: PrepackedWeights | None, experts: int, rows: int, k: int,
-                    device: torch.device, what: str) -> PrepackedWeights | None:
-    """Validate a caller's prepacked copy against the weights of the call."""
+                    device: torch.device, what: str, packed: torch.Tensor | None = None,
+                    block_scales: torch.Tensor | None = None) -> PrepackedWeights | None:
+    """Validate a caller's prepacked copy against the weights of the call
+    (shapes and device; with ``packed`` / ``block_scales``, also that the copy
+    was made from those tensors and they have not been written since)."""
     if pre is None:
         return None
     if not isinstance(pre, PrepackedWeights):
@@ -91,4 +122,9 @@ def check_prepacked(pre: PrepackedWeights | None, experts: int, rows: int, k: in
         raise ValueError(
             f"{what}: prepacked copy is for {pre.experts} x {pre.rows} x {pre.k} on "
             f"{pre.nibbles.device}, the call has {experts} x {rows} x {k} on {device}")
+    if packed is not None and block_scales is not None and not pre.is_current(packed,
+                                                                              block_scales):
+        raise ValueError(
+            f"{what}: prepacked copy is stale: it was made from other weight tensors, or "
+            f"they were written in place since; call prepack_w4a16 again")
     return pre

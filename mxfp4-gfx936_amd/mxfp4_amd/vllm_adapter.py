@@ -16,7 +16,10 @@ After loading, each layer also gets a prepacked copy of its weights
 (``prepack_w4a16``: the fragment-ordered layout its prefill GEMMs read;
 bitwise-equal results) as ``layer.mxfp4_prepacked`` (dense) or
 ``layer.mxfp4_prepacked13`` / ``layer.mxfp4_prepacked2`` (MoE), unless
-``MXFP4_GFX950_PREPACK=0`` or the weights are not on a GPU.
+``MXFP4_GFX950_PREPACK=0`` or the weights are not on a GPU.  The apply hooks
+prepack again when a parameter was replaced or written in place since
+(its version counter moved); after writes through ``param.data``, which
+PyTorch does not version, call ``refresh_prepacked(layer)``.
 
 Call ``install()`` before constructing ``vllm.LLM``.  ``install(dense_cls,
 moe_cls)`` patches the given classes instead of importing vLLM's (how the
@@ -106,12 +109,36 @@ def _bf16_moe_layer(x, w13, s13, w2, s2, topk_weights, topk_ids):
 
 
 def _prepacked(packed, scales):
-    """The prepacked copy of loaded weights, or None where it does not apply."""
+    """The prepacked copy of loaded weights, or None where it does not apply.
+    Made from the parameters the apply hooks pass (not their ``.data``,
+    whose version counter is a separate one), so an in-place update of a
+    parameter shows as a stale copy."""
     if os.getenv("MXFP4_GFX950_PREPACK", "1") == "0" or not packed.is_cuda:
         return None
     if (packed.shape[-1] * 2) % 64 != 0:
         return None
     return prepack_w4a16(packed, scales)
+
+
+def _current(layer, attr, packed, scales):
+    """The layer's prepacked copy ``attr``, made again first if the weights
+    were replaced or written in place since it was made."""
+    pre = getattr(layer, attr, None)
+    if pre is not None and not pre.is_current(packed, scales):
+        pre = _prepacked(packed, scales)
+        setattr(layer, attr, pre)
+    return pre
+
+
+def refresh_prepacked(layer) -> None:
+    """Prepack a layer's weights again, e.g. after a weight update written
+    through ``param.data`` (which PyTorch does not version)."""
+    if hasattr(layer, "mxfp4_prepacked"):
+        layer.mxfp4_prepacked = _prepacked(layer.weight_packed, layer.weight_scale)
+    if hasattr(layer, "mxfp4_prepacked13"):
+        layer.mxfp4_prepacked13 = _prepacked(layer.w13_weight, layer.w13_weight_scale)
+    if hasattr(layer, "mxfp4_prepacked2"):
+        layer.mxfp4_prepacked2 = _prepacked(layer.w2_weight, layer.w2_weight_scale)
 
 
 def _dense_process_weights_after_loading(self, layer):
@@ -120,7 +147,7 @@ def _dense_process_weights_after_loading(self, layer):
     del self
     layer.weight_packed = Parameter(layer.weight_packed.data, requires_grad=False)
     layer.weight_scale = Parameter(layer.weight_scale.data, requires_grad=False)
-    layer.mxfp4_prepacked = _prepacked(layer.weight_packed.data, layer.weight_scale.data)
+    layer.mxfp4_prepacked = _prepacked(layer.weight_packed, layer.weight_scale)
 
 
 def _dense_apply_weights(self, layer, x, bias=None, input_quant_args=None,
@@ -129,8 +156,8 @@ def _dense_apply_weights(self, layer, x, bias=None, input_quant_args=None,
     del self, input_quant_args, silu_quant_args
     if _active() == "reference":
         return _bf16_linear(x, layer.weight_packed, layer.weight_scale, bias)
-    return linear_mxfp4_soft(x, layer.weight_packed, layer.weight_scale, bias,
-                             prepacked=getattr(layer, "mxfp4_prepacked", None))
+    pre = _current(layer, "mxfp4_prepacked", layer.weight_packed, layer.weight_scale)
+    return linear_mxfp4_soft(x, layer.weight_packed, layer.weight_scale, bias, prepacked=pre)
 
 
 def _moe_process_weights_after_loading(self, layer):
@@ -143,8 +170,8 @@ def _moe_process_weights_after_loading(self, layer):
     layer.w2_weight_scale = Parameter(layer.w2_weight_scale.data, requires_grad=False)
     delattr(layer, "w13_weight_packed")
     delattr(layer, "w2_weight_packed")
-    layer.mxfp4_prepacked13 = _prepacked(layer.w13_weight.data, layer.w13_weight_scale.data)
-    layer.mxfp4_prepacked2 = _prepacked(layer.w2_weight.data, layer.w2_weight_scale.data)
+    layer.mxfp4_prepacked13 = _prepacked(layer.w13_weight, layer.w13_weight_scale)
+    layer.mxfp4_prepacked2 = _prepacked(layer.w2_weight, layer.w2_weight_scale)
 
 
 def _moe_apply(self, layer, x, topk_weights, topk_ids, use_nn_moe=False):
@@ -156,10 +183,11 @@ def _moe_apply(self, layer, x, topk_weights, topk_ids, use_nn_moe=False):
     if _active() == "reference":
         return _bf16_moe_layer(x, layer.w13_weight, layer.w13_weight_scale, layer.w2_weight,
                                layer.w2_weight_scale, topk_weights, topk_ids)
+    pre13 = _current(layer, "mxfp4_prepacked13", layer.w13_weight, layer.w13_weight_scale)
+    pre2 = _current(layer, "mxfp4_prepacked2", layer.w2_weight, layer.w2_weight_scale)
     return moe_layer(x, layer.w13_weight, layer.w13_weight_scale, layer.w2_weight,
                      layer.w2_weight_scale, topk_weights, topk_ids, activation=layer.activation,
-                     prepacked13=getattr(layer, "mxfp4_prepacked13", None),
-                     prepacked2=getattr(layer, "mxfp4_prepacked2", None))
+                     prepacked13=pre13, prepacked2=pre2)
 
 
 def _vllm_classes():

@@ -281,10 +281,17 @@ def assert_layer_blocks(y, o, ref, routes, what, row_block=128):
             f"routes {routes[i, :, j].double().cpu().numpy().tolist()}")
     frac = (rel > O.ELEM_TOL).double().mean().item()
     assert frac <= 1e-3, f"{what} {frac:.2e} of elements beyond {O.ELEM_TOL}"
-    nb = y2.shape[0] // row_block
-    on = o2[:nb * row_block].reshape(nb, -1).norm(dim=1)
-    err = (y2 - o2)[:nb * row_block].reshape(nb, -1).norm(dim=1) / on
-    rerr = (r2 - o2)[:nb * row_block].reshape(nb, -1).norm(dim=1) / on
+    # blocks of row_block tokens, the last one partial (zero rows padded in
+    # add nothing to its norms)
+    nb = (y2.shape[0] + row_block - 1) // row_block
+    pad = nb * row_block - y2.shape[0]
+
+    def blocks(t):
+        t = torch.nn.functional.pad(t, (0, 0, 0, pad))
+        return t.reshape(nb, -1)
+    on = blocks(o2).norm(dim=1)
+    err = blocks(y2 - o2).norm(dim=1) / on
+    rerr = blocks(r2 - o2).norm(dim=1) / on
     assert err.max() <= O.NORM_TOL, f"{what} norm-wise {err.max():.3e}"
     # below a tenth of the bar both sit at the rounding-flip noise of the
     # same rounding points, where "no worse" is a coin toss

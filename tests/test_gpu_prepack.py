@@ -98,3 +98,43 @@ def test_prepacked_copy_of_other_weights_is_refused(moe_weights):
         mx.moe_layer(x, w13, s13, w2, s2, tw, ti, prepacked13=p2, prepacked2=p13)
     with pytest.raises(ValueError, match="prepacked copy"):
         mx.linear_mxfp4_soft(x, w13[0], s13[0], prepacked=p13)
+
+
+def test_stale_prepacked_copy_is_refused_and_the_hooks_refresh():
+    # an in-place update of the weights makes the copy stale: the operator
+    # refuses it, and the vLLM apply hook prepacks again before the call
+    import types
+
+    from torch.nn import Parameter
+
+    from mxfp4_amd import vllm_adapter as va
+    rng = np.random.default_rng(401)
+    m, k, n = 512, 1024, 640  # a prefill grid (it reads the prepacked copy)
+    w0, s0 = rand_mxfp4(rng, (n,), k)
+    w1, _ = rand_mxfp4(rng, (n,), k)
+    x = cuda(rand_act(402, (m, k)))
+    w, s = cuda(w0), cuda(s0)
+    pre = mx.prepack_w4a16(w, s)
+    assert torch.equal(mx.linear_mxfp4_soft(x, w, s, prepacked=pre), mx.linear_mxfp4_soft(x, w, s))
+    w.copy_(cuda(w1))
+    with pytest.raises(ValueError, match="stale"):
+        mx.linear_mxfp4_soft(x, w, s, prepacked=pre)
+    pre = mx.prepack_w4a16(w, s)
+    assert torch.equal(mx.linear_mxfp4_soft(x, w, s, prepacked=pre), mx.linear_mxfp4_soft(x, w, s))
+
+    layer = types.SimpleNamespace(weight_packed=cuda(w0), weight_scale=cuda(s0))
+    va._dense_process_weights_after_loading(None, layer)
+    first = layer.mxfp4_prepacked
+    y0 = va._dense_apply_weights(None, layer, x)
+    assert torch.equal(y0, mx.linear_mxfp4_soft(x, cuda(w0), cuda(s0)))
+    assert layer.mxfp4_prepacked is first
+    with torch.no_grad():  # a weight sync writing the parameter in place
+        layer.weight_packed.copy_(cuda(w1))
+    y1 = va._dense_apply_weights(None, layer, x)
+    assert layer.mxfp4_prepacked is not first
+    assert torch.equal(y1, mx.linear_mxfp4_soft(x, cuda(w1), cuda(s0)))
+    # a write through .data is not versioned: refresh_prepacked picks it up
+    layer.weight_packed.data.copy_(cuda(w0))
+    va.refresh_prepacked(layer)
+    assert torch.equal(va._dense_apply_weights(None, layer, x), y0)
+    assert isinstance(layer.weight_packed, Parameter)

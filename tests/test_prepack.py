@@ -68,3 +68,70 @@ def test_check_prepacked_rejects_mismatches():
         check_prepacked(pre, 2, 16, 64, cpu, "t")
     with pytest.raises(TypeError, match="prepack_w4a16"):
         check_prepacked((pre.nibbles, pre.scales), 1, 16, 64, cpu, "t")
+
+
+def test_check_prepacked_rejects_stale_copies():
+    from mxfp4_amd.prepack import _source_of
+    cpu = torch.device("cpu")
+    w = torch.zeros((16, 32), dtype=torch.uint8)
+    s = torch.zeros((16, 2), dtype=torch.uint8)
+    pre = PrepackedWeights(torch.zeros(512, dtype=torch.uint8), torch.zeros(32), 1, 16, 64,
+                           (_source_of(w), _source_of(s)))
+    assert check_prepacked(pre, 1, 16, 64, cpu, "t", w, s) is pre
+    # a view of the same storage at the same address and version is the same weights
+    assert check_prepacked(pre, 1, 16, 64, cpu, "t", w.view(16, 32), s) is pre
+    # other tensors of the same shape
+    with pytest.raises(ValueError, match="stale"):
+        check_prepacked(pre, 1, 16, 64, cpu, "t", w.clone(), s)
+    # an in-place write bumps the version counter (also through a view)
+    w[0, 0] = 1
+    with pytest.raises(ValueError, match="stale"):
+        check_prepacked(pre, 1, 16, 64, cpu, "t", w, s)
+    pre2 = PrepackedWeights(pre.nibbles, pre.scales, 1, 16, 64, (_source_of(w), _source_of(s)))
+    s[:, 1:].fill_(3)
+    with pytest.raises(ValueError, match="stale"):
+        check_prepacked(pre2, 1, 16, 64, cpu, "t", w, s)
+    # inference-mode tensors keep no version: the address is still compared
+    with torch.inference_mode():
+        wi = torch.zeros((16, 32), dtype=torch.uint8)
+    pre3 = PrepackedWeights(pre.nibbles, pre.scales, 1, 16, 64, (_source_of(wi), _source_of(s)))
+    assert check_prepacked(pre3, 1, 16, 64, cpu, "t", wi, s) is pre3
+    with pytest.raises(ValueError, match="stale"):
+        check_prepacked(pre3, 1, 16, 64, cpu, "t", w, s)
+
+
+def test_vllm_hooks_prepack_again_after_an_update(monkeypatch):
+    # the apply hooks' freshness rule with a stand-in for the device prepack
+    from torch.nn import Parameter
+
+    from mxfp4_amd import vllm_adapter as V
+    from mxfp4_amd.prepack import _source_of
+    made = []
+
+    def fake_prepacked(packed, scales):
+        made.append(1)
+        return PrepackedWeights(torch.zeros(1), torch.zeros(1), 1, packed.shape[0],
+                                packed.shape[1] * 2, (_source_of(packed), _source_of(scales)))
+
+    monkeypatch.setattr(V, "_prepacked", fake_prepacked)
+
+    class Layer:
+        pass
+    layer = Layer()
+    layer.weight_packed = Parameter(torch.zeros((16, 32), dtype=torch.uint8), requires_grad=False)
+    layer.weight_scale = Parameter(torch.zeros((16, 2), dtype=torch.uint8), requires_grad=False)
+    layer.mxfp4_prepacked = V._prepacked(layer.weight_packed, layer.weight_scale)
+    first = layer.mxfp4_prepacked
+    assert V._current(layer, "mxfp4_prepacked", layer.weight_packed, layer.weight_scale) is first
+    with torch.no_grad():
+        layer.weight_packed.copy_(torch.ones((16, 32), dtype=torch.uint8))
+    second = V._current(layer, "mxfp4_prepacked", layer.weight_packed, layer.weight_scale)
+    assert second is not first and layer.mxfp4_prepacked is second and len(made) == 2
+    # current again: no further prepack
+    assert V._current(layer, "mxfp4_prepacked", layer.weight_packed, layer.weight_scale) is second
+    # a replaced parameter is other weights
+    layer.weight_scale = Parameter(torch.ones((16, 2), dtype=torch.uint8), requires_grad=False)
+    V._current(layer, "mxfp4_prepacked", layer.weight_packed, layer.weight_scale)
+    assert len(made) == 3
+    V.refresh_prepacked(layer)
+    assert len(made) == 4

@@ -115,17 +115,21 @@ def test_apply_paths_call_the_operators(monkeypatch):
     assert va._dense_apply_weights(object(), dense, "x", "b", input_quant_args=1,
                                    silu_quant_args=2) == "y"
     assert calls[-1] == ("linear", ("x", "W", "S", "b"), {"prepacked": None})
-    dense.mxfp4_prepacked = "P"  # the copy process_weights_after_loading made
+    class Copy:  # stands in for the copy process_weights_after_loading made
+        def is_current(self, packed, scales):
+            return True
+    P, P13, P2 = Copy(), Copy(), Copy()
+    dense.mxfp4_prepacked = P
     va._dense_apply_weights(object(), dense, "x")
-    assert calls[-1] == ("linear", ("x", "W", "S", None), {"prepacked": "P"})
+    assert calls[-1] == ("linear", ("x", "W", "S", None), {"prepacked": P})
     moe = types.SimpleNamespace(activation="silu", w13_weight="A", w13_weight_scale="As",
                                 w2_weight="B", w2_weight_scale="Bs")
     assert va._moe_apply(object(), moe, "x", "tw", "ti", use_nn_moe=True) == "z"
     assert calls[-1] == ("moe", ("x", "A", "As", "B", "Bs", "tw", "ti"),
                          {"activation": "silu", "prepacked13": None, "prepacked2": None})
-    moe.mxfp4_prepacked13, moe.mxfp4_prepacked2 = "P13", "P2"
+    moe.mxfp4_prepacked13, moe.mxfp4_prepacked2 = P13, P2
     va._moe_apply(object(), moe, "x", "tw", "ti")
-    assert calls[-1][2] == {"activation": "silu", "prepacked13": "P13", "prepacked2": "P2"}
+    assert calls[-1][2] == {"activation": "silu", "prepacked13": P13, "prepacked2": P2}
     moe.activation = "gelu"
     with pytest.raises(NotImplementedError, match="silu"):
         va._moe_apply(object(), moe, "x", "tw", "ti")
