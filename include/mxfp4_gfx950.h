@@ -51,7 +51,9 @@ enum {
   MXFP4_DT_F16 = 2,
   MXFP4_DT_U8 = 3, /* packed E2M1 pairs */
   MXFP4_DT_I32 = 4,
-  MXFP4_DT_I64 = 5
+  MXFP4_DT_I64 = 5,
+  MXFP4_DT_F8E4M3 = 6, /* OCP FP8 E4M3 (torch.float8_e4m3fn) */
+  MXFP4_DT_F8E5M2 = 7  /* OCP FP8 E5M2 (torch.float8_e5m2) */
 };
 
 /* Quantizer rounding modes for mxfp4_quant. */
@@ -182,7 +184,12 @@ int mxfp4_moe_route(const float* logits, int64_t m, int num_experts, int64_t row
  * Routed grouped GEMM -- the compute of fused_moe_mxfp4_soft, soft:379-494,
  * and of AITER's fused_moe_mxfp4, aiter:28-364.
  *   a: activations [a_rows, k]: BF16/F16/F32 (a_dtype), or packed u8
- *      [a_rows, k/2] with a_mx u8 [a_rows, k/32] (a_dtype = MXFP4_DT_U8).
+ *      [a_rows, k/2] with a_mx u8 [a_rows, k/32] (a_dtype = MXFP4_DT_U8), or
+ *      OCP FP8 [a_rows, k] (a_dtype = MXFP4_DT_F8E4M3 / F8E5M2; the e4m3 /
+ *      e5m2 formats aiter:11-20 maps into tl.dot_scaled) with a_mx u8
+ *      [a_rows, k/32] or NULL (every scale 1) -- packed and FP8 A run on the
+ *      block-scaled f8f6f4 MFMA, each product A * 2^(sa-127) * B * 2^(sb-127)
+ *      exact, FP32 accumulation.
  *   b u8 [num_experts, n, k/2], b_mx u8 [num_experts, n, k/32], contiguous.
  *   c: output rows indexed by route id, c + route * c_row_stride, of c_dtype
  *      (BF16, F16 or F32; the compute type of soft:405-407).

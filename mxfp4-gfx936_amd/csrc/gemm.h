@@ -20,8 +20,8 @@ enum Epilogue {
 };
 
 struct GemmArgs {
-  const void* a;        // activations (T) or packed u8
-  const uint8_t* a_mx;  // packed A scales [a_rows, k/32] (W4A4 only)
+  const void* a;        // activations (T), packed u8 or FP8
+  const uint8_t* a_mx;  // A scales [a_rows, k/32] (packed / FP8 A; FP8: may be null = 1)
   int64_t a_rows;       // activation rows addressable through `a`
   int64_t lda;          // A row stride, elements (bytes for packed A)
   int64_t lda_mx;       // A scale row stride, bytes
@@ -67,7 +67,14 @@ struct GemmArgs {
   // set on the copy a prefill kernel receives: b / bs / b_e / bs_e are then
   // the prepacked arrays
   int32_t prepacked;
+  // block-scaled (W4A4) GEMMs: activation format, 0 = packed E2M1, 1 = FP8
+  // E4M3, 2 = FP8 E5M2 (FP8 rows are k bytes)
+  int32_t a_fp8;
 };
+
+// MFMA operand format code of the block-scaled f8f6f4 instructions for
+// GemmArgs::a_fp8 (0 -> E2M1 = 4, 1 -> E4M3 = 0, 2 -> E5M2 = 1).
+constexpr int mfma_fmt_of(int a_fp8) { return a_fp8 == 0 ? 4 : a_fp8 - 1; }
 
 // Bytes of the prepacked layout of `experts` weight matrices of `rows` x k
 // (k % 64 == 0): nibble blocks, then scale operands.

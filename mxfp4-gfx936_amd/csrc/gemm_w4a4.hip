@@ -6,31 +6,39 @@
 // E2M1 product times its two power-of-two scales is exact, accumulation is
 // FP32, and scales/route weights apply to the FP32 accumulator.
 //
-// Lane layout of the 16x16x128 FP4 MFMA (verified on the device): lane l
-// supplies row/column l % 16 and K = (l/16)*32 .. +32 as 16 bytes (low
-// nibble first) in the first four dwords of its operand, and the E8M0 byte
-// of that 32-block in byte 0 of its scale operand.
+// Lane layout of the 16x16x128 MFMA (verified on the device): lane l
+// supplies row/column l % 16 and the E8M0 byte of K block l/16 (K =
+// (l/16)*32 .. +32) in byte 0 of its scale operand.  An E2M1 operand holds
+// that block as 16 bytes (low nibble first) in its first four dwords; an
+// FP8 operand (E4M3 / E5M2: the activation formats of aiter:11-20) holds K =
+// (l/16)*16 .. +16 in dwords 0-3 and K = 64 + (l/16)*16 .. +16 in dwords 4-7
+// (a one-wave probe with one-hot E2M1 rows and distinct FP8 bytes read the
+// mapping off the products), the scale still that of block l/16.
 //
 // Tiling: 256-thread workgroups, 4 waves as WGM x WGN, wave tile FM x FN
-// MFMA blocks; each 128-deep K stage stages A and B packed tiles (64 B per
-// row) and their scale bytes in LDS, double buffered.
+// MFMA blocks; each 128-deep K stage stages A and B tiles (64 B per packed
+// row, 128 B per FP8 row) and their scale bytes in LDS, double buffered.
+// AF: MFMA format of A (4 = E2M1, 0 = E4M3, 1 = E5M2).
 #include "gemm.h"
 
 namespace mx {
 namespace {
 
-template <typename TO, int FM, int FN, int WGM, int WGN>
+template <typename TO, int FM, int FN, int WGM, int WGN, int AF>
 __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
   constexpr int BM = WGM * FM * 16;
   constexpr int BN = WGN * FN * 16;
   constexpr int BK = 128;
   constexpr int LD = 80;  // bytes per LDS row: 64 data + 16 pad (conflict-free b128 reads)
-  constexpr int A_CHUNKS = BM * 4;  // 16-byte chunks per stage
+  constexpr bool F8 = AF != 4;
+  constexpr int ACPR = F8 ? 8 : 4;  // 16-byte A chunks per row and stage
+  constexpr int LDA = F8 ? 144 : LD;
+  constexpr int A_CHUNKS = BM * ACPR;  // 16-byte chunks per stage
   constexpr int B_CHUNKS = BN * 4;
   static_assert(WGM * WGN == 4, "4 waves");
   static_assert(BN == 128, "tile config");
 
-  __shared__ __attribute__((aligned(16))) uint8_t As[2][BM][LD];
+  __shared__ __attribute__((aligned(16))) uint8_t As[2][BM][LDA];
   __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN][LD];
   __shared__ uint8_t Sa[2][BM][4];
   __shared__ uint8_t Sb[2][BN][4];
@@ -67,10 +75,10 @@ __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
     a_src[i] = nullptr;
     as_src[i] = nullptr;
     if (c < A_CHUNKS) {
-      const RowInfo ri = row_info(g, pos0 + (c >> 2));
+      const RowInfo ri = row_info(g, pos0 + c / ACPR);
       if (ri.valid) {
         a_src[i] = static_cast<const uint8_t*>(g.a) + ri.a_row * g.lda;
-        as_src[i] = g.a_mx + ri.a_row * g.lda_mx;
+        as_src[i] = g.a_mx ? g.a_mx + ri.a_row * g.lda_mx : nullptr;  // FP8: null = scale 1
       }
     }
   }
@@ -92,10 +100,13 @@ __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < A_PER; ++i) {
       const int c = tid + i * 256;
-      const int k = kt * BK + (c & 3) * 32;
-      const bool ok = a_src[i] && k < g.k;
-      areg[i] = ok ? *reinterpret_cast<const i32x4*>(a_src[i] + (k >> 1)) : i32x4{0, 0, 0, 0};
-      asreg[i] = ok ? as_src[i][k >> 5] : (uint8_t)127;
+      // packed: chunk c % 4 is 32-block c % 4; FP8: chunk c % 8 holds K
+      // (c % 8) * 16 .. +16 of 32-block (c % 8) / 2
+      const int k = F8 ? kt * BK + (c % ACPR) * 16 : kt * BK + (c & 3) * 32;
+      const bool ok = a_src[i] && (k & ~31) < g.k;
+      areg[i] = ok ? *reinterpret_cast<const i32x4*>(a_src[i] + (F8 ? k : (k >> 1)))
+                   : i32x4{0, 0, 0, 0};
+      asreg[i] = (ok && as_src[i]) ? as_src[i][k >> 5] : (uint8_t)127;
     }
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
@@ -111,8 +122,8 @@ __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
     for (int i = 0; i < A_PER; ++i) {
       const int c = tid + i * 256;
       if (c < A_CHUNKS) {
-        *reinterpret_cast<i32x4*>(&As[buf][c >> 2][(c & 3) * 16]) = areg[i];
-        Sa[buf][c >> 2][c & 3] = asreg[i];
+        *reinterpret_cast<i32x4*>(&As[buf][c / ACPR][(c % ACPR) * 16]) = areg[i];
+        if (!F8 || (c & 1) == 0) Sa[buf][c / ACPR][F8 ? (c % ACPR) / 2 : (c & 3)] = asreg[i];
       }
     }
 #pragma unroll
@@ -142,7 +153,12 @@ __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
     for (int fm = 0; fm < FM; ++fm) {
       const int r = wm * FM * 16 + fm * 16 + c16;
       const i32x4 v = *reinterpret_cast<const i32x4*>(&As[buf][r][grp * 16]);
-      af[fm] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
+      if constexpr (F8) {
+        const i32x4 w = *reinterpret_cast<const i32x4*>(&As[buf][r][(4 + grp) * 16]);
+        af[fm] = i32x8{v[0], v[1], v[2], v[3], w[0], w[1], w[2], w[3]};
+      } else {
+        af[fm] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
+      }
       asc[fm] = Sa[buf][r][grp];
     }
 #pragma unroll
@@ -154,7 +170,7 @@ __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
         acc[fm][fn] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            af[fm], bf, acc[fm][fn], 4, 4, 0, asc[fm], 0, bsc);
+            af[fm], bf, acc[fm][fn], AF, 4, 0, asc[fm], 0, bsc);
     }
     if (kt + 1 < nk) store_lds(buf ^ 1);
     __syncthreads();
@@ -181,7 +197,7 @@ __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
   }
 }
 
-template <typename TO>
+template <typename TO, int AF>
 int launch_w4a4_typed(const GemmArgs& g, hipStream_t st) {
   const int64_t cap = g.m;
   const bool routed = g.sorted_ids != nullptr;
@@ -209,12 +225,21 @@ int launch_w4a4_typed(const GemmArgs& g, hipStream_t st) {
   }
   dim3 grid((unsigned)ntiles, (unsigned)(gy > 0 ? gy : 1));
   switch (bm) {
-    case 128: w4a4_tiled<TO, 4, 4, 2, 2><<<grid, 256, 0, st>>>(g); break;
-    case 64: w4a4_tiled<TO, 2, 4, 2, 2><<<grid, 256, 0, st>>>(g); break;
-    case 32: w4a4_tiled<TO, 1, 4, 2, 2><<<grid, 256, 0, st>>>(g); break;
-    default: w4a4_tiled<TO, 1, 2, 1, 4><<<grid, 256, 0, st>>>(g); break;
+    case 128: w4a4_tiled<TO, 4, 4, 2, 2, AF><<<grid, 256, 0, st>>>(g); break;
+    case 64: w4a4_tiled<TO, 2, 4, 2, 2, AF><<<grid, 256, 0, st>>>(g); break;
+    case 32: w4a4_tiled<TO, 1, 4, 2, 2, AF><<<grid, 256, 0, st>>>(g); break;
+    default: w4a4_tiled<TO, 1, 2, 1, 4, AF><<<grid, 256, 0, st>>>(g); break;
   }
   return launch_status("w4a4 launch");
+}
+
+template <int AF>
+int launch_tiled_out(const GemmArgs& g, int out_dtype, hipStream_t st) {
+  switch (out_dtype) {
+    case MXFP4_DT_BF16: return launch_w4a4_typed<__bf16, AF>(g, st);
+    case MXFP4_DT_F16: return launch_w4a4_typed<_Float16, AF>(g, st);
+    default: return launch_w4a4_typed<float, AF>(g, st);
+  }
 }
 
 }  // namespace
@@ -224,11 +249,14 @@ int launch_w4a4(const GemmArgs& g, int out_dtype, hipStream_t st) {
     const int cfg = p4_supported(g) ? p4_choose(g, out_dtype) : -1;
     if (cfg >= 0) return launch_w4a4_pf(g, out_dtype, cfg, st);
   }
-  switch (out_dtype) {
-    case MXFP4_DT_BF16: return launch_w4a4_typed<__bf16>(g, st);
-    case MXFP4_DT_F16: return launch_w4a4_typed<_Float16>(g, st);
-    case MXFP4_DT_F32: return launch_w4a4_typed<float>(g, st);
-    default: set_error("w4a4: unsupported output dtype %d", out_dtype); return MXFP4_ERR_TYPE;
+  if (out_dtype != MXFP4_DT_BF16 && out_dtype != MXFP4_DT_F16 && out_dtype != MXFP4_DT_F32) {
+    set_error("w4a4: unsupported output dtype %d", out_dtype);
+    return MXFP4_ERR_TYPE;
+  }
+  switch (g.a_fp8) {
+    case 1: return launch_tiled_out<0>(g, out_dtype, st);
+    case 2: return launch_tiled_out<1>(g, out_dtype, st);
+    default: return launch_tiled_out<4>(g, out_dtype, st);
   }
 }
 

@@ -35,6 +35,13 @@
 //   B operand, so a lane owns 4 consecutive output columns of one row; the
 //   epilogue stages the finished tile in LDS and writes 16-byte chunks.
 //
+// * FP8 activations (AF = 0 E4M3 / 1 E5M2, aiter:11-20): A rows are K
+//   bytes, so a stage holds 128 x KS bytes of each A row; the fragment of
+//   lane l at step h is two chunks, K h*128 + (l/16)*16 .. +16 and h*128 +
+//   64 + (l/16)*16 .. +16 (the FP8 operand layout of the 16x16x128 MFMA), in
+//   slots swizzled by row so the 16 rows of a read cover all banks.  A
+//   missing A scale (FP8 without A_mx_scale) is the constant 127 (1.0).
+//
 // Requirements (else the register-staged w4a4_tiled runs): K % 128 == 0,
 // 16-byte aligned A / B rows and scale rows 4-byte aligned, operands below
 // 2 GiB.
@@ -43,14 +50,15 @@
 namespace mx {
 namespace {
 
-template <int WGM, int WGN, int FM, int FN, int STAGES, int SQ, int KS>
+template <int WGM, int WGN, int FM, int FN, int STAGES, int SQ, int KS, int AF = 4>
 struct P4Shape {
   static constexpr int NW = WGM * WGN;
   static constexpr int NT = 64 * NW;
   static constexpr int BM = WGM * FM * 16;
   static constexpr int BN = WGN * FN * 16;
-  static constexpr int RB = 64 * KS;  // bytes of a row's stage
-  static constexpr int A_STAGE = BM * RB;
+  static constexpr int RB = 64 * KS;  // bytes of a (packed) row's stage
+  static constexpr int RBA = (AF == 4 ? 64 : 128) * KS;  // bytes of an A row's stage
+  static constexpr int A_STAGE = BM * RBA;
   static constexpr int B_STAGE = BN * RB;
   static constexpr int A_TOT = A_STAGE / 1024;  // 1 KB wave-loads per stage
   static constexpr int B_TOT = B_STAGE / 1024;
@@ -71,9 +79,10 @@ struct P4Shape {
   static constexpr int PIPE = SC_BASE + SBUFS * (SA_BUF + SB_BUF);
 };
 
-template <typename TO, int WGM, int WGN, int FM, int FN, int STAGES, int MINB, int SQ, int KS>
+template <typename TO, int WGM, int WGN, int FM, int FN, int STAGES, int MINB, int SQ, int KS,
+          int AF>
 __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int nbm, int nbn) {
-  typedef P4Shape<WGM, WGN, FM, FN, STAGES, SQ, KS> S;
+  typedef P4Shape<WGM, WGN, FM, FN, STAGES, SQ, KS, AF> S;
   constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
   static_assert(FN % 2 == 0, "2-byte outputs pair the column blocks");
   static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 stages");
@@ -111,27 +120,34 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
   }
 
   const i32x4 rA = make_rsrc(g.a, (uint32_t)(g.a_rows * g.lda));
-  const i32x4 rSA = make_rsrc(g.a_mx, (uint32_t)(g.a_rows * g.lda_mx));
+  // FP8 A without scales: the scale loads read nothing (offsets past an
+  // empty range of the weight scales) and the operand is 127
+  const bool amx = g.a_mx != nullptr;
+  const i32x4 rSA = amx ? make_rsrc(g.a_mx, (uint32_t)(g.a_rows * g.lda_mx)) : make_rsrc(g.bs, 0u);
   const i32x4 rB = make_rsrc(g.b + expert * g.b_e, (uint32_t)((int64_t)g.n * g.b_n));
   const i32x4 rSB = make_rsrc(g.bs + expert * g.bs_e, (uint32_t)((int64_t)g.n * g.bs_n));
 
   // per-lane offsets for stage 0 (stage kt adds kt * RB / kt * 4 * KS as
   // the scalar offset); wave-load q of a stage is issued by wave q % NW;
   // lane l fills slot l % (4 KS) of tile row q * 16 / KS + l / (4 KS)
-  constexpr int CPR = 4 * KS;  // 16-byte chunks per row stage
-  auto chunk_of = [&](int trow) {
-    const int slot = lane % CPR;
-    return KS == 1 ? slot : slot ^ ((trow >> 1) & 7);
+  constexpr int CPR = 4 * KS;        // 16-byte chunks per packed row stage
+  constexpr int CPRA = S::RBA / 16;  // ... per A row stage
+  // slot <-> chunk of a row's stage (an involution): rows of 4 chunks
+  // unswizzled, of 8 XOR (row / 2) % 8, of 16 XOR row % 16
+  auto swz = [&](int cpr, int trow) {
+    return cpr == 4 ? 0 : (cpr == 8 ? (trow >> 1) & 7 : trow & 15);
   };
+  auto chunk_of = [&](int trow) { return (lane % CPR) ^ swz(CPR, trow); };
   uint32_t a_off[S::A_PER];
 #pragma unroll
   for (int j = 0; j < S::A_PER; ++j) {
     const int q = j * S::NW + wave;
-    const int row = q * (16 / KS) + lane / CPR;
+    const int row = q * (64 / CPRA) + lane / CPRA;
     a_off[j] = kOOB;
     if (q < S::A_TOT) {
       const RowInfo ri = row_info(g, pos0 + row);
-      if (ri.valid) a_off[j] = (uint32_t)(ri.a_row * g.lda) + chunk_of(row) * 16;
+      if (ri.valid)
+        a_off[j] = (uint32_t)(ri.a_row * g.lda) + ((lane % CPRA) ^ swz(CPRA, row)) * 16;
     }
   }
   uint32_t b_off[S::B_PER];
@@ -151,7 +167,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
     s_off[j] = kOOB;
     if (q < S::SA_TOT) {
       const int row = q * 64 + lane;
-      if (row < BM) {
+      if (row < BM && amx) {
         const RowInfo ri = row_info(g, pos0 + row);
         if (ri.valid) s_off[j] = (uint32_t)(ri.a_row * g.lda_mx);
       }
@@ -170,7 +186,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
       const int q = j * S::NW + wave;
       if (S::A_TOT % S::NW == 0 || q < S::A_TOT)
         llvm_amdgcn_raw_buffer_load_lds(rA, lds_ptr(base + q * 1024), 16, (int)a_off[j],
-                                        kt * S::RB, 0, 0);
+                                        kt * S::RBA, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < S::B_PER; ++j) {
@@ -203,7 +219,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
   // h*4 + grp (in its slot); weight fragment fn likewise; scale bytes grp of
   // those rows.  The slot swizzle depends on the row only through c16.
   auto slot_of = [&](int h) { return KS == 1 ? grp : (h * 4 + grp) ^ ((c16 >> 1) & 7); };
-  const int a_rd = (wm * FM * 16 + c16) * S::RB;
+  // FP8 A: chunks h*8 + grp and h*8 + 4 + grp (swizzled by the fragment row,
+  // which differs from c16 by a multiple of 16)
+  auto slot_a = [&](int chunk) { return chunk ^ swz(CPRA, c16); };
+  const int a_rd = (wm * FM * 16 + c16) * S::RBA;
   const int b_rd = (wn * FN * 16 + c16) * S::RB;
   const int sa_rd = (wm * FM * 16 + c16) * 4 * SQ + grp;
   const int sb_rd = (wn * FN * 16 + c16) * 4 * SQ + grp;
@@ -246,9 +265,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
       int asc[FM];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
-        const i32x4 v = *reinterpret_cast<const i32x4*>(As + a_rd + slot + fm * 16 * S::RB);
-        af[fm] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
-        asc[fm] = Sa[sa_rd + fm * 16 * 4 * SQ];
+        if constexpr (AF == 4) {
+          const i32x4 v = *reinterpret_cast<const i32x4*>(As + a_rd + slot + fm * 16 * S::RBA);
+          af[fm] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
+        } else {
+          const uint8_t* ar = As + a_rd + fm * 16 * S::RBA;
+          const i32x4 v = *reinterpret_cast<const i32x4*>(ar + slot_a(h * 8 + grp) * 16);
+          const i32x4 w = *reinterpret_cast<const i32x4*>(ar + slot_a(h * 8 + 4 + grp) * 16);
+          af[fm] = i32x8{v[0], v[1], v[2], v[3], w[0], w[1], w[2], w[3]};
+        }
+        asc[fm] = amx ? (int)Sa[sa_rd + fm * 16 * 4 * SQ] : 127;
       }
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) {
@@ -258,7 +284,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
           acc[fm][fn] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              bf, af[fm], acc[fm][fn], 4, 4, 0, bsc, 0, asc[fm]);
+              bf, af[fm], acc[fm][fn], 4, AF, 0, bsc, 0, asc[fm]);
       }
     }
   }
@@ -331,10 +357,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
 }
 
 // STAGES1: stages of the per-stage-scale kernel; STAGES4 x KS4: stages and
-// steps per stage of the grouped-scale kernel
-template <typename TO, int WGM, int WGN, int FM, int FN, int MINB, int STAGES1, int STAGES4, int KS4>
+// steps per stage of the grouped-scale kernel; AF: activation format
+template <typename TO, int AF, int WGM, int WGN, int FM, int FN, int MINB, int STAGES1, int STAGES4,
+          int KS4>
 int launch_cfg(const GemmArgs& g, hipStream_t st) {
-  typedef P4Shape<WGM, WGN, FM, FN, STAGES1, 1, 1> S;
+  typedef P4Shape<WGM, WGN, FM, FN, STAGES1, 1, 1, AF> S;
   const int nbn = (g.n + S::BN - 1) / S::BN;
   int64_t nbm = (g.m + S::BM - 1) / S::BM;
   if (g.sorted_ids) nbm = (nbm + 7) / 8 * 8;  // every XCD covers 1/8 of the capacity (tile_of)
@@ -344,21 +371,30 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
     return MXFP4_ERR_VALUE;
   }
   // 16-byte scale groups: whole groups of aligned rows (K % 512 == 0)
-  const bool sq4 = g.k % 512 == 0 && g.lda_mx % 16 == 0 && g.bs_n % 16 == 0 &&
-                   !(reinterpret_cast<uintptr_t>(g.a_mx) & 15) &&
+  const bool amx_ok = g.a_mx == nullptr ||
+                      (g.lda_mx % 16 == 0 && !(reinterpret_cast<uintptr_t>(g.a_mx) & 15));
+  const bool sq4 = g.k % 512 == 0 && amx_ok && g.bs_n % 16 == 0 &&
                    !(reinterpret_cast<uintptr_t>(g.bs) & 15) && g.bs_e % 16 == 0;
   if (sq4)
-    w4a4_pf<TO, WGM, WGN, FM, FN, STAGES4, MINB, 4, KS4>
+    w4a4_pf<TO, WGM, WGN, FM, FN, STAGES4, MINB, 4, KS4, AF>
         <<<(unsigned)nwg, S::NT, 0, st>>>(g, (int)nbm, nbn);
   else
-    w4a4_pf<TO, WGM, WGN, FM, FN, STAGES1, MINB, 1, 1>
+    w4a4_pf<TO, WGM, WGN, FM, FN, STAGES1, MINB, 1, 1, AF>
         <<<(unsigned)nwg, S::NT, 0, st>>>(g, (int)nbm, nbn);
   return launch_status("w4a4 prefill launch");
 }
 
-template <typename TO>
+template <typename TO, int AF>
 int launch_typed(const GemmArgs& g, int cfg, hipStream_t st) {
-  {
+  if constexpr (AF != 4) {
+    // FP8 activations: A rows twice the bytes, 128-deep stages (LDS of
+    // 256 x 256: 3 x (32 + 16) KB + 16 KB of scales)
+    switch (cfg) {
+      case P4_256x256: return launch_cfg<TO, AF, 2, 4, 8, 4, 1, 3, 3, 1>(g, st);
+      case P4_128x128: return launch_cfg<TO, AF, 1, 4, 8, 2, 2, 3, 3, 1>(g, st);
+      default: return launch_cfg<TO, AF, 1, 4, 4, 2, 2, 2, 2, 1>(g, st);  // P4_64x128
+    }
+  } else {
     // Measured (8192 x 4096 x 4096, bf16 out): 2 x 4 waves of 128 x 64,
     // grouped scales, 2 stages of 256 ~3.5-3.6 PFLOP/s (8192^3: 4.07), 3
     // stages of 128 ~3.2 (3.56); per-stage scales, 3 stages of 128 ~3.0;
@@ -366,9 +402,9 @@ int launch_typed(const GemmArgs& g, int cfg, hipStream_t st) {
     // 128 x 64 (256 x 512) does not fit the register file.  128 x 128 tiles
     // at M = 2048, K = N = 4096: 256-deep stages 2.56 vs 2.23 PFLOP/s.
     switch (cfg) {
-      case P4_256x256: return launch_cfg<TO, 2, 4, 8, 4, 1, 3, 2, 2>(g, st);
-      case P4_128x128: return launch_cfg<TO, 1, 4, 8, 2, 2, 2, 2, 2>(g, st);
-      default: return launch_cfg<TO, 1, 4, 4, 2, 2, 2, 2, 1>(g, st);  // P4_64x128
+      case P4_256x256: return launch_cfg<TO, 4, 2, 4, 8, 4, 1, 3, 2, 2>(g, st);
+      case P4_128x128: return launch_cfg<TO, 4, 1, 4, 8, 2, 2, 2, 2, 2>(g, st);
+      default: return launch_cfg<TO, 4, 1, 4, 4, 2, 2, 2, 2, 1>(g, st);  // P4_64x128
     }
   }
 }
@@ -400,11 +436,20 @@ int p4_choose(const GemmArgs& g, int out_dtype) {
   return -1;
 }
 
-int launch_w4a4_pf(const GemmArgs& g, int out_dtype, int cfg, hipStream_t st) {
+template <int AF>
+int launch_out(const GemmArgs& g, int out_dtype, int cfg, hipStream_t st) {
   switch (out_dtype) {
-    case MXFP4_DT_BF16: return launch_typed<__bf16>(g, cfg, st);
-    case MXFP4_DT_F16: return launch_typed<_Float16>(g, cfg, st);
-    default: return launch_typed<float>(g, cfg, st);
+    case MXFP4_DT_BF16: return launch_typed<__bf16, AF>(g, cfg, st);
+    case MXFP4_DT_F16: return launch_typed<_Float16, AF>(g, cfg, st);
+    default: return launch_typed<float, AF>(g, cfg, st);
+  }
+}
+
+int launch_w4a4_pf(const GemmArgs& g, int out_dtype, int cfg, hipStream_t st) {
+  switch (g.a_fp8) {
+    case 1: return launch_out<0>(g, out_dtype, cfg, st);
+    case 2: return launch_out<1>(g, out_dtype, cfg, st);
+    default: return launch_out<4>(g, out_dtype, cfg, st);
   }
 }
 

@@ -601,12 +601,14 @@ int do_align(const void* ids, int ids_dtype, int64_t n, int num_experts, int blo
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 int dispatch_gemm(const GemmArgs& g, int a_dtype, int c_dtype, int epi, hipStream_t st) {
-  if (a_dtype == MXFP4_DT_U8) {
+  if (a_dtype == MXFP4_DT_U8 || a_dtype == MXFP4_DT_F8E4M3 || a_dtype == MXFP4_DT_F8E5M2) {
     if (epi != EPI_STORE) {
-      set_error("packed activations support the plain epilogue only");
+      set_error("packed / FP8 activations support the plain epilogue only");
       return MXFP4_ERR_VALUE;
     }
-    return launch_w4a4(g, c_dtype, st);
+    GemmArgs g8 = g;
+    g8.a_fp8 = a_dtype == MXFP4_DT_F8E4M3 ? 1 : (a_dtype == MXFP4_DT_F8E5M2 ? 2 : 0);
+    return launch_w4a4(g8, c_dtype, st);
   }
   if (c_dtype == MXFP4_DT_F32) {
     if (epi != EPI_STORE) {
@@ -714,14 +716,18 @@ int check_routed_args(const void* a, int a_dtype, int64_t a_row_stride, const ui
     set_error("packed MXFP4 activations require A_mx_scale");
     return MXFP4_ERR_VALUE;
   }
+  if (a_dtype != MXFP4_DT_U8 && a_dtype != MXFP4_DT_F8E4M3 && a_dtype != MXFP4_DT_F8E5M2 &&
+      a_dtype != MXFP4_DT_F32 && a_dtype != MXFP4_DT_BF16 && a_dtype != MXFP4_DT_F16) {
+    set_error("unsupported activation dtype %d", a_dtype);
+    return MXFP4_ERR_TYPE;
+  }
   if (k <= 0 || k % 32 != 0 || n <= 0 || n > 0x7FFFFFFF || k > 0x7FFFFFFF || num_experts < 1 ||
       top_k < 1 || block_m < 16 || block_m % 16 != 0 || em < 0 || em % block_m != 0) {
     set_error("moe gemm: invalid sizes (n %lld, k %lld, block_m %d, em %lld)", (long long)n,
               (long long)k, block_m, (long long)em);
     return MXFP4_ERR_VALUE;
   }
-  if (!aligned16(a) || !aligned16(b) || (a_dtype != MXFP4_DT_U8 && (a_row_stride * elem_size(a_dtype)) % 16) ||
-      (a_dtype == MXFP4_DT_U8 && a_row_stride % 16)) {
+  if (!aligned16(a) || !aligned16(b) || (a_row_stride * elem_size(a_dtype)) % 16) {
     set_error("moe gemm: activation/weight rows must be 16-byte aligned");
     return MXFP4_ERR_VALUE;
   }
@@ -850,7 +856,8 @@ extern "C" int mxfp4_fused_moe_workspace_size(int64_t m, int top_k, int64_t num_
               (long long)num_experts);
     return MXFP4_ERR_VALUE;
   }
-  const bool w4a16 = a_dtype != MXFP4_DT_U8 && c_dtype != MXFP4_DT_F32;
+  const bool w4a16 = (a_dtype == MXFP4_DT_BF16 || a_dtype == MXFP4_DT_F16) &&
+                     c_dtype != MXFP4_DT_F32;
   *bytes = plan_soft(m * top_k, num_experts, w4a16).total;
   return MXFP4_OK;
 }
@@ -873,7 +880,8 @@ extern "C" int mxfp4_fused_moe(const void* a, int a_dtype, int64_t a_rows, int64
     return MXFP4_ERR_VALUE;
   }
   const int64_t routes = m * top_k;
-  const bool w4a16 = a_dtype != MXFP4_DT_U8 && c_dtype != MXFP4_DT_F32;
+  const bool w4a16 = (a_dtype == MXFP4_DT_BF16 || a_dtype == MXFP4_DT_F16) &&
+                     c_dtype != MXFP4_DT_F32;
   const SoftPlan p = plan_soft(routes, num_experts, w4a16);
   int rc = check_routed_args(a, a_dtype, a_row_stride, a_mx, b, num_experts, n, k, c_dtype, top_k,
                              p.block_m, p.max_sorted);

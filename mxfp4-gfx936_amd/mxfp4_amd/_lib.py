@@ -19,7 +19,7 @@ LIB_PATH = os.environ.get("MXFP4_GFX950_LIB", os.path.join(_HERE, "libmxfp4_gfx9
 
 # include/mxfp4_gfx950.h
 OK, ERR_TYPE, ERR_VALUE, ERR_NOT_IMPLEMENTED, ERR_RUNTIME, ERR_HIP = range(6)
-DT_F32, DT_BF16, DT_F16, DT_U8, DT_I32, DT_I64 = range(6)
+DT_F32, DT_BF16, DT_F16, DT_U8, DT_I32, DT_I64, DT_F8E4M3, DT_F8E5M2 = range(8)
 QUANT_TIES_AWAY, QUANT_RNE = 0, 1
 ABI_VERSION = 1
 
@@ -30,6 +30,8 @@ _DTYPE_CODES = {
     torch.uint8: DT_U8,
     torch.int32: DT_I32,
     torch.int64: DT_I64,
+    torch.float8_e4m3fn: DT_F8E4M3,
+    torch.float8_e5m2: DT_F8E5M2,
 }
 
 _P = ctypes.c_void_p

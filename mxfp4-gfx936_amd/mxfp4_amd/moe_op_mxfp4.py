@@ -11,10 +11,20 @@ one expert per ``config["BLOCK_SIZE_M"]`` block, expert -1 writes zeros,
 dispatches gfx936 to the soft op (aiter:390-410), this module is the gfx950
 branch: it runs the HIP kernels of libmxfp4_gfx950.so.
 
+Activations: bf16 / fp16 / fp32 (converted to C.dtype), packed MXFP4
+(uint8 with ``A_mx_scale``), or OCP FP8 -- ``torch.float8_e4m3fn`` /
+``torch.float8_e5m2``, the "e4m3" / "e5m2" formats aiter:11-20 hands to
+``tl.dot_scaled`` -- which run on gfx950's block-scaled f8f6f4 MFMA with the
+FP8 operand format, each product exact, FP32 accumulation.  FP8 A may come
+without ``A_mx_scale`` (the reference's host path, aiter:413-418: every
+scale 1) or with E8M0 scales [M, K/32] (the kernel's micro-scaled A,
+aiter:182-214, 329-338, which the reference's host assert does not let
+through).
+
 Differences, all explicit: swizzled MX scales raise NotImplementedError
 (the reference kernel marks them TODO, aiter:69-70, 189-205); ``config``
 contributes only BLOCK_SIZE_M (tile shapes are chosen by the library);
-``compute_type`` must name C's dtype.
+``compute_type`` must name C's dtype; FP8 A with ``A_mx_scale`` is accepted.
 """
 
 from __future__ import annotations
@@ -24,7 +34,7 @@ from typing import Any, Dict
 import torch
 
 from . import _lib
-from .moe_op_mxfp4_soft import _moe_gemm_launch, _prepare_moe_operands
+from .moe_op_mxfp4_soft import _FP8_DTYPES, _moe_gemm_launch, _prepare_moe_operands
 
 _COMPUTE_NAMES = {
     torch.bfloat16: ("bfloat16", "bf16"),
@@ -72,7 +82,7 @@ def fused_moe_mxfp4(
     assert B_scale is not None
     if A.dtype == torch.uint8:
         assert A_mx_scale is not None, "A_mx_scale should exist when A is mxfp4"
-    else:
+    elif A.dtype not in _FP8_DTYPES:
         assert A_mx_scale is None, "A_mx_scale should not exist when A is not mxfp4"
     assert B_mx_scale is not None
     if B.dtype != torch.uint8:
@@ -91,7 +101,8 @@ def fused_moe_mxfp4(
         raise RuntimeError("num_tokens_post_padded must hold one value")
 
     act, act_mx, b, b_mx, a_scale, b_scale, weights, ids = _prepare_moe_operands(
-        A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights, topk_ids, top_k)
+        A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights, topk_ids, top_k,
+        fp8_activations=True)
     device = _lib.require_device(A, B, C, sorted_token_ids, expert_ids, num_tokens_post_padded)
     num_routes = ids.numel()
     if em == 0 or C.numel() == 0:

@@ -243,9 +243,15 @@ def _moe_gemm_launch(A, A_mx_scale, B, B_mx_scale, C2d, A_scale, B_scale, topk_w
             _lib.stream_of(device)))
 
 
+_FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
+
+
 def _prepare_moe_operands(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights,
-                          topk_ids, top_k):
-    """Shared shape checks and layout normalisation for the routed GEMM."""
+                          topk_ids, top_k, fp8_activations=False):
+    """Shared shape checks and layout normalisation for the routed GEMM.
+    ``fp8_activations`` (AITER's entry): OCP FP8 A (e4m3 / e5m2) stays in
+    its format, with optional E8M0 A_mx_scale [M, K/32], for the
+    block-scaled MFMA; otherwise non-packed A is converted to C.dtype."""
     matmul_dtype = C.dtype
     if B.ndim != 3 or B_mx_scale.shape != (B.shape[0], B.shape[1], B.shape[2] * 2 // 32):
         raise ValueError("B must be [E, N, K/2] with B_mx_scale [E, N, K/32]")
@@ -272,6 +278,18 @@ def _prepare_moe_operands(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, top
             raise RuntimeError("packed activations must be [M, K/2] with A_mx_scale [M, K/32]")
         act = _lib.aligned(A)
         act_mx = A_mx_scale.contiguous()
+    elif fp8_activations and A.dtype in _FP8_DTYPES:
+        if A.ndim != 2 or A.shape[1] != logical_k:
+            raise RuntimeError(f"activations must be [M, {logical_k}], got {tuple(A.shape)}")
+        if A_mx_scale is not None:
+            if A_mx_scale.dtype != torch.uint8:
+                raise TypeError(f"A_mx_scale must be uint8, got {A_mx_scale.dtype}")
+            if A_mx_scale.shape != (A.shape[0], logical_k // 32):
+                raise ValueError("one E8M0 scale is required for every 32 FP8 values")
+            act_mx = A_mx_scale.contiguous()
+        else:
+            act_mx = None
+        act = _lib.aligned(A)
     else:
         if A_mx_scale is not None:
             raise ValueError("unpacked activations must not provide A_mx_scale")

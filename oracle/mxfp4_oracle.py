@@ -191,6 +191,38 @@ def dequant_values(packed, scales, dtype: str) -> np.ndarray:
     return round_to_dtype(v, dtype)
 
 
+def fp8_values(codes: np.ndarray, fmt: str) -> np.ndarray:
+    """OCP FP8 byte -> exact value (float64): the activation formats that
+    aiter:11-20 hands to ``tl.dot_scaled`` as "e4m3" (``tl.float8e4nv``,
+    torch.float8_e4m3fn: bias 7, no infinities, S.1111.111 is NaN) and "e5m2"
+    (``tl.float8e5``, torch.float8_e5m2: bias 15, IEEE-style inf / NaN).
+    Closed form from the bit fields; subnormals for exponent field 0."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    if fmt == "e4m3":
+        e, m = (c >> 3) & 0xF, c & 0x7
+        mag = np.where(e == 0, np.ldexp(m / 8.0, -6), np.ldexp(1.0 + m / 8.0, e - 7))
+        mag = np.where((e == 0xF) & (m == 0x7), np.nan, mag)
+    elif fmt == "e5m2":
+        e, m = (c >> 2) & 0x1F, c & 0x3
+        mag = np.where(e == 0, np.ldexp(m / 4.0, -14), np.ldexp(1.0 + m / 4.0, e - 15))
+        mag = np.where(e == 0x1F, np.where(m == 0, np.inf, np.nan), mag)
+    else:
+        raise ValueError(f"unsupported fp8 format {fmt}")
+    return sign * mag
+
+
+def fp8_scaled_values(codes: np.ndarray, scales: np.ndarray | None, fmt: str) -> np.ndarray:
+    """FP8 activations times their E8M0 block scales (one per 32 along the
+    last axis; None = every scale 1): the exact values the block-scaled MFMA
+    multiplies (aiter:206-214, 329-338 with an FP8 A)."""
+    v = fp8_values(codes, fmt)
+    if scales is None:
+        return v
+    s = np.repeat(e8m0_to_f32(np.asarray(scales, np.uint8)).astype(np.float64), BLOCK, axis=-1)
+    return v * s
+
+
 # ----------------------------------------------------------------------------
 # Quantizers
 # ----------------------------------------------------------------------------

@@ -593,3 +593,179 @@ def test_moe_layer_fused_decode_top_k(m, top_k, hidden, inter, e, dtype):
     safe = O.moe_layer_safe(x, t(w13), t(s13), t(w2), t(s2), w, ids)
     assert_layer_parity(y, oracle, safe, what=f"fused decode top_k={top_k} {dtype}",
                         routes=routes, fmt="f16" if dtype == torch.float16 else "bf16")
+
+
+# ---------------------------------------------------------------- FP8 activations
+
+_FP8 = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+
+
+def _assert_fp8_parity(y, oracle, a_val, wp, ws, ids, alpha, what, out_fmt="bf16"):
+    """Parity bar of the FP8-activation GEMMs.  The block-scaled MFMA adds
+    each group of 8 consecutive K products keeping ~12 bits below the
+    group's largest product (measured with one MFMA: 448 + 2^-3 -> 448.125,
+    448 + 2^-6 -> 448, 448 - 448 + 2^-9 -> 0; sums across groups keep FP32
+    precision), which E2M1 x E2M1 products never exceed but FP8's wider
+    range can.  So besides norm-wise <= NORM_TOL, each element must be
+    within ELEM_TOL (denominator floor 1e-3 * rms) or within
+    2^-10 * sum over its K groups of max|a| * max|w| (times the scales and
+    route weight) plus one step of the output."""
+    y = y.float().cpu().numpy().astype(np.float64) if isinstance(y, torch.Tensor) else y
+    e = O.parity_errors(y, oracle)
+    assert e["norm_rel"] <= O.NORM_TOL, f"{what} norm-wise {e['norm_rel']:.3e}"
+    m, k = a_val.shape
+    amax = np.abs(a_val).reshape(m, k // 8, 8).max(-1)                       # [m, G]
+    w_val = O.dequant_values(wp, ws, "bf16")                                  # [E, n, k]
+    ne, n = w_val.shape[:2]
+    wmax = np.abs(w_val).reshape(ne, n, k // 8, 8).max(-1)                    # [E, n, G]
+    ids = np.asarray(ids)
+    budget = np.zeros(oracle.shape)
+    for ex in range(ne):
+        t, sl = np.nonzero(ids == ex)
+        budget[t, sl] = (amax[t] @ wmax[ex].T) * np.asarray(alpha)[t, sl, None] * 2.0 ** -10
+    floor = 1e-3 * np.sqrt(np.mean(oracle * oracle))
+    diff = np.abs(y - oracle)
+    bad = ((diff / np.maximum(np.abs(oracle), floor) > O.ELEM_TOL)
+           & (diff > budget + (O.format_ulp(oracle, out_fmt) if out_fmt else 0.0)))
+    assert not bad.any(), (f"{what}: {int(bad.sum())} elements beyond {O.ELEM_TOL} and the "
+                           f"MFMA's group-alignment budget (max elementwise {e['elem_rel']:.3e})")
+
+
+def _mxfp8_quant(a: np.ndarray, fmt: str):
+    """MXFP8 test data: per 32 along K, scale byte 127 + floor(log2 amax) - emax
+    (emax 7 for e4m3, 14 for e5m2: the block's largest magnitude lands in
+    [2^emax, 2^(emax+1)), inside the format), values rounded to the format by
+    torch's own conversion."""
+    emax = 7 if fmt == "e4m3" else 14
+    blocks = a.reshape(a.shape[0], -1, 32)
+    amax = np.abs(blocks).max(-1)
+    e = np.floor(np.log2(np.maximum(amax, 2.0 ** -100))).astype(np.int64) - emax
+    scales = np.clip(127 + e, 1, 254).astype(np.uint8)
+    q = blocks / np.exp2(scales.astype(np.float64) - 127)[..., None]
+    codes = torch.from_numpy(q.reshape(a.shape).astype(np.float32)).to(_FP8[fmt])
+    return codes.view(torch.uint8).numpy(), scales
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("block_m", [16, 32, 64, 128])
+@pytest.mark.parametrize("k", [1024, 384, 160])
+def test_aiter_entry_fp8_every_byte_at_every_k(fmt, block_m, k):
+    # one-hot weights (row j of each expert is 1.0 at K = j) make every
+    # output a single exact product, fp8(A[t, j]) * 2^(sa - 127) * 2^(sb - 127),
+    # checked bit for bit in FP32: each activation row holds all finite
+    # bytes of the format across K, so every byte value is decoded at
+    # every K position, through the MFMA's FP8 operand layout and the A / B
+    # scale of each 32-block.  K = 1024 takes the grouped-scale
+    # direct-to-LDS kernel on 64- / 128-row blocks, 384 its per-stage-scale
+    # variant, 160 (not a multiple of 128) the register-staged kernel, as do
+    # 16- / 32-row blocks; an expert -1 block writes zeros
+    rng = np.random.default_rng(block_m * 7 + k + (1 if fmt == "e5m2" else 0))
+    m, e, top_k = 96, 3, 2
+    n = k
+    finite = [b for b in range(256) if not ((b & 0x7F) == 0x7F if fmt == "e4m3"
+                                            else (b & 0x7C) == 0x7C)]
+    ab = np.stack([np.resize(np.roll(finite, 13 * t), k) for t in range(m)]).astype(np.uint8)
+    amx = rng.integers(120, 135, size=(m, k // 32), dtype=np.uint8)
+    codes = np.zeros((e, n, k), dtype=np.uint8)
+    codes[:, np.arange(n), np.arange(n)] = 2  # E2M1 1.0
+    wp = (codes[..., 0::2] | (codes[..., 1::2] << 4)).astype(np.uint8)
+    ws = rng.integers(124, 131, size=(e, n, k // 32), dtype=np.uint8)
+    w, ids = _route(m, e, top_k, 300 + block_m)
+    srt, exp_, npp = O.make_routing(ids.numpy(), block_m=block_m, num_experts=e)
+    exp_ = exp_.copy()
+    exp_[exp_ == 1] = -1
+    C = torch.full((m, top_k, n), 3.0, dtype=torch.float32, device="cuda")
+    mx.fused_moe_mxfp4(torch.from_numpy(ab).view(_FP8[fmt]).cuda(), cuda(wp), C,
+                       torch.ones(1, device="cuda"), torch.ones(e, device="cuda"), cuda(amx),
+                       cuda(ws), cuda(w), cuda(ids), cuda(srt), cuda(exp_), cuda(npp), False,
+                       top_k, False, False, {"BLOCK_SIZE_M": block_m}, torch.float32)
+    ids_np = ids.numpy()
+    a_val = O.fp8_scaled_values(ab, amx, fmt)                          # [m, k]
+    b_scale = O.e8m0_to_f32(ws).astype(np.float64)                      # [e, n, k/32]
+    want = a_val[:, None, :] * np.take_along_axis(
+        np.repeat(b_scale, 32, axis=-1), np.arange(n)[None, :, None], axis=-1)[..., 0][ids_np]
+    want[ids_np == 1] = 0.0
+    got = C.cpu().numpy().astype(np.float64)
+    assert np.array_equal(got, want), (
+        f"{int((got != want).sum())} of {got.size} outputs differ (fp8 {fmt}, block {block_m}, "
+        f"k {k})")
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("block_m", [16, 64, 128])
+@pytest.mark.parametrize("scaled", [True, False], ids=["a_mx", "no_a_mx"])
+def test_aiter_entry_fp8_activations(fmt, block_m, scaled):
+    # MXFP8 activations from N(0, 1) data (with A_mx_scale) or FP8 values of
+    # N(0, 1) data without scales (the reference's host path), route
+    # weights, an expert -1 block, against the FP64 oracle
+    rng = np.random.default_rng(block_m * 3 + (1 if fmt == "e5m2" else 0) + (5 if scaled else 0))
+    m, n, e, top_k, k = 300, 320, 4, 2, 1024
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rng.standard_normal((m, k))
+    if scaled:
+        ab, amx = _mxfp8_quant(a, fmt)
+    else:
+        ab = torch.from_numpy(a.astype(np.float32)).to(_FP8[fmt]).view(torch.uint8).numpy()
+        amx = None
+    w, ids = _route(m, e, top_k, 300 + block_m)
+    srt, exp_, npp = O.make_routing(ids.numpy(), block_m=block_m, num_experts=e)
+    exp_ = exp_.copy()
+    exp_[exp_ == 1] = -1
+    C = torch.full((m, top_k, n), 3.0, dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4(torch.from_numpy(ab).view(_FP8[fmt]).cuda(), cuda(wp), C,
+                       torch.tensor([0.5], device="cuda"), torch.linspace(1, 2, e, device="cuda"),
+                       cuda(amx) if scaled else None, cuda(ws), cuda(w), cuda(ids), cuda(srt),
+                       cuda(exp_), cuda(npp), True, top_k, False, False,
+                       {"BLOCK_SIZE_M": block_m}, torch.bfloat16)
+    ids_np = ids.numpy()
+    a_val = O.fp8_scaled_values(ab, amx, fmt)
+    oracle = O.fused_moe_fp64(a_val, wp, ws, 0.5, np.linspace(1, 2, e), w.numpy(), ids_np, True)
+    oracle[ids_np == 1] = 0.0
+    alpha = 0.5 * np.linspace(1, 2, e)[ids_np] * w.numpy()
+    _assert_fp8_parity(C, oracle, a_val, wp, ws, ids_np, alpha, f"fp8 {fmt} block {block_m}")
+
+
+@pytest.mark.parametrize("c_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("block_m", [32, 128])
+def test_aiter_entry_fp8_output_dtypes(c_dtype, block_m):
+    rng = np.random.default_rng(17 + block_m)
+    m, n, e, top_k, k = 200, 192, 3, 2, 512
+    wp, ws = rand_mxfp4(rng, (e, n), k, lo=118, hi=126)
+    ab, amx = _mxfp8_quant(rng.standard_normal((m, k)), "e4m3")
+    w, ids = _route(m, e, top_k, 31 + block_m)
+    srt, exp_, npp = O.make_routing(ids.numpy(), block_m=block_m, num_experts=e)
+    C = torch.empty((m, top_k, n), dtype=c_dtype, device="cuda")
+    mx.fused_moe_mxfp4(torch.from_numpy(ab).view(torch.float8_e4m3fn).cuda(), cuda(wp), C,
+                       torch.ones(1, device="cuda"), torch.ones(e, device="cuda"), cuda(amx),
+                       cuda(ws), cuda(w), cuda(ids), cuda(srt), cuda(exp_), cuda(npp), False,
+                       top_k, False, False, {"BLOCK_SIZE_M": block_m}, c_dtype)
+    a_val = O.fp8_scaled_values(ab, amx, "e4m3")
+    oracle = O.fused_moe_fp64(a_val, wp, ws, 1.0, np.ones(e), w.numpy(), ids.numpy(), False)
+    assert np.isfinite(oracle).all()
+    _assert_fp8_parity(C, oracle, a_val, wp, ws, ids.numpy(), np.ones(ids.shape),
+                       f"fp8 out {c_dtype}", out_fmt="f16" if c_dtype == torch.float16 else None)
+
+
+def test_soft_op_fp8_activations_convert_to_compute_dtype():
+    # soft:472-475: unpacked A is A.to(C.dtype) (exact for e4m3 / e5m2 in
+    # bf16), and A_mx_scale must be None
+    rng = np.random.default_rng(55)
+    m, n, e, top_k, k = 40, 96, 5, 2, 256
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    ab = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(
+        torch.float8_e5m2).view(torch.uint8).numpy()
+    A = torch.from_numpy(ab).view(torch.float8_e5m2).cuda()
+    w, ids = _route(m, e, top_k, 56)
+    C = torch.empty((m, top_k, n), dtype=torch.bfloat16, device="cuda")
+    mx.fused_moe_mxfp4_soft(A, cuda(wp), C, torch.ones(1, device="cuda"),
+                            torch.ones(e, device="cuda"), None, cuda(ws), cuda(w), cuda(ids),
+                            _empty(), _empty(), _empty(), True, top_k, False, False)
+    oracle = O.fused_moe_fp64(O.fp8_values(ab, "e5m2"), wp, ws, 1.0, np.ones(e), w.numpy(),
+                              ids.numpy(), True)
+    assert_parity(C, oracle, what="soft op fp8 A")
+    with pytest.raises(ValueError, match="must not provide A_mx_scale"):
+        mx.fused_moe_mxfp4_soft(A, cuda(wp), C, torch.ones(1, device="cuda"),
+                                torch.ones(e, device="cuda"),
+                                torch.full((m, k // 32), 127, dtype=torch.uint8, device="cuda"),
+                                cuda(ws), cuda(w), cuda(ids), _empty(), _empty(), _empty(), True,
+                                top_k, False, False)

@@ -449,3 +449,34 @@ def test_format_ulp_is_the_grid_spacing():
                                   np.nextafter(f, np.float32(np.inf)).astype(np.float64) - f)
     assert O.format_ulp(np.array([0.0]), "bf16")[0] == 2.0 ** -133
     assert O.format_ulp(np.array([np.nan, np.inf]), "bf16").tolist() == [0.0, 0.0]
+
+
+@pytest.mark.parametrize("fmt,tdt", [("e4m3", torch.float8_e4m3fn), ("e5m2", torch.float8_e5m2)])
+def test_fp8_decode_matches_torch_on_every_byte(fmt, tdt):
+    # the FP8 activation formats of aiter:11-20: every one of the 256 bytes
+    # decoded from the bit fields equals torch's own float8 -> float32
+    # conversion (NaN bytes: NaN-ness), plus a few values by hand
+    codes = np.arange(256, dtype=np.uint8)
+    ours = O.fp8_values(codes, fmt)
+    theirs = torch.from_numpy(codes).view(tdt).float().numpy().astype(np.float64)
+    assert np.array_equal(np.isnan(ours), np.isnan(theirs))
+    fin = ~np.isnan(ours)
+    assert np.array_equal(ours[fin], theirs[fin])
+    assert np.array_equal(np.signbit(ours[fin]), np.signbit(theirs[fin]))  # -0
+    if fmt == "e4m3":
+        assert O.fp8_values(np.array([0x7E, 0x01, 0x38, 0xB8]), fmt).tolist() == \
+            [448.0, 2.0 ** -9, 1.0, -1.0]
+        assert np.isnan(O.fp8_values(np.array([0x7F, 0xFF]), fmt)).all()
+    else:
+        assert O.fp8_values(np.array([0x7B, 0x01, 0x3C, 0x7C]), fmt).tolist() == \
+            [57344.0, 2.0 ** -16, 1.0, np.inf]
+
+
+def test_fp8_scaled_values_apply_the_block_scale():
+    codes = np.full((2, 64), 0x38, dtype=np.uint8)  # e4m3 1.0
+    scales = np.array([[127, 130], [0, 254]], dtype=np.uint8)
+    v = O.fp8_scaled_values(codes, scales, "e4m3")
+    assert np.array_equal(v[0, :32], np.ones(32)) and np.array_equal(v[0, 32:], np.full(32, 8.0))
+    assert np.array_equal(v[1, :32], np.full(32, 2.0 ** -127))
+    assert np.array_equal(v[1, 32:], np.full(32, 2.0 ** 127))
+    assert np.array_equal(O.fp8_scaled_values(codes, None, "e4m3"), np.ones((2, 64)))
