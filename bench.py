@@ -195,6 +195,30 @@ def traffic_probe() -> int:
     return 0
 
 
+def headline_probe() -> int:
+    """Headline launches for trace and counter runs: qkv M=4096, K=2048,
+    N=5120 with the prepacked copy, then on the checkpoint layout, each
+    after an untimed clock ramp, 20 launches."""
+    import numpy as np
+    import torch
+
+    import mxfp4_amd as mx
+    mx._lib.load()
+    m, k, n = 4096, 2048, 5120
+    rng = np.random.default_rng(20260810 + 1)
+    (w, s), = rand_weights(rng, (n,), k)
+    x = randn_bf16(20260810, (m, k))
+    pre = mx.prepack_w4a16(w, s)
+    for name, q in (("prepacked", pre), ("checkpoint", None)):
+        ramp_clocks(lambda: mx.linear_mxfp4_soft(x, w, s, prepacked=q))
+        for _ in range(20):
+            mx.linear_mxfp4_soft(x, w, s, prepacked=q)
+        torch.cuda.synchronize()
+        log(f"headline probe {name} done")
+    print(json.dumps({"probe": "headline", "m": m, "k": k, "n": n}))
+    return 0
+
+
 def decode_probe() -> int:
     """Decode launches for counter and trace runs of the bandwidth-bound
     kernels: dense W4A16 GEMV (qkv M=1 and 8, o_proj M=1) over rotated weight
@@ -701,6 +725,8 @@ def main() -> int:
                     help="time the headline GEMM on random vs zero / constant inputs")
     ap.add_argument("--moe-probe", action="store_true",
                     help="only run MoE layer prefill launches for trace runs")
+    ap.add_argument("--headline-probe", action="store_true",
+                    help="only run headline launches (prepacked, then checkpoint layout)")
     ap.add_argument("--soft-probe", action="store_true",
                     help="only run soft-op / AITER-entry launches for trace runs")
     ap.add_argument("--w4a4-probe", action="store_true",
@@ -723,6 +749,8 @@ def main() -> int:
         return w4a4_probe()
     if args.soft_probe:
         return soft_probe()
+    if args.headline_probe:
+        return headline_probe()
 
     import numpy as np
     import torch
