@@ -1041,6 +1041,15 @@ int pf_choose(const GemmArgs& g, int epi) {
   // (512 tokens, 64-row blocks: 64 x 128 59.0 / 35.9 vs 64 x 256 66.9 /
   // 39.1; 32-row blocks: 32 x 128 67.7 vs 32 x 256 75.3 and 32 x 512
   // 117 us; 1024 tokens, down: 64 x 256 49.3 vs 64 x 128 51.9).
+  // The SiLU GEMM of the MoE layer on the checkpoint layout: BM x 128 tiles
+  // on 32- / 64-row blocks, 128 x 256 on 128-row ones (MoE layer, graph
+  // replays: 512 tokens, 64-row blocks, 64 x 128 126.1 vs 64 x 384 140.6
+  // us; 256 tokens, 32-row blocks, 32 x 128 108.8 vs 32 x 256 112.2; 1024
+  // tokens, 128-row blocks, 128 x 256 160.2 vs 128 x 128 165.1)
+  if (routed && epi == EPI_SILU_MUL && !pf_prepacked_usable(g)) {
+    if (allowed(128)) return PF_128x256;
+    return allowed(64) ? PF_64x128 : PF_32x128;
+  }
   if (routed && epi == EPI_STORE && !pf_prepacked_usable(g)) {
     if (allowed(128)) return PF_128x256;
     const int bm = allowed(64) ? 64 : 32;

@@ -640,7 +640,7 @@ struct LayerPlan {
 };
 
 LayerPlan plan_layer(int64_t m, int top_k, int num_experts, int64_t hidden, int64_t inter,
-                     int64_t esize) {
+                     int64_t esize, bool prepacked) {
   LayerPlan p;
   p.routes = m * top_k;
   const double avg = (double)p.routes / (double)num_experts;
@@ -655,6 +655,13 @@ LayerPlan plan_layer(int64_t m, int top_k, int num_experts, int64_t hidden, int6
   // win only where their tiles just fill whole rounds (1536 tokens 166 vs
   // 182 us, 1664 170 vs 184 us).
   p.block_m = avg <= 1.5 ? 16 : (avg <= 32.0 ? 32 : 64);
+  // Checkpoint-layout weights (no prepacked copies) take the fused soft
+  // op's rule -- 32-row blocks up to 28 routes per expert, 64 up to 56,
+  // 128 above -- with BM x 128 SiLU tiles on 32- and 64-row blocks and
+  // 128 x 256 on 128-row ones (pf_choose).  Layer, graph replays (E=128,
+  // top-8, H=2048, I=768): 256 tokens 112.0 -> 108.8 us, 512 153.2 ->
+  // 126.1, 1024 185.5 -> 160.2, 2048 246.7 -> 242.5, 4096 418.2 -> 414.4.
+  if (!prepacked) p.block_m = avg <= 1.5 ? 16 : (avg <= 28.0 ? 32 : (avg <= 56.0 ? 64 : 128));
   align_capacity(p.routes, num_experts, p.block_m, &p.max_sorted, &p.max_blocks, &p.nchunks);
   int64_t off = 0;
   p.off_counts = off; off = round_up(off + (p.nchunks > 0 ? p.nchunks : 1) * num_experts * 4, 256);
@@ -1043,7 +1050,10 @@ extern "C" int mxfp4_moe_layer_workspace_size(int64_t m, int top_k, int num_expe
     set_error("moe layer: invalid sizes");
     return MXFP4_ERR_VALUE;
   }
-  *bytes = plan_layer(m, top_k, num_experts, hidden, inter, 2).total;
+  // either weight layout's plan fits (the caller may pass prepacked copies)
+  const int64_t a = plan_layer(m, top_k, num_experts, hidden, inter, 2, true).total;
+  const int64_t b = plan_layer(m, top_k, num_experts, hidden, inter, 2, false).total;
+  *bytes = a > b ? a : b;
   return MXFP4_OK;
 }
 
@@ -1085,7 +1095,7 @@ extern "C" int mxfp4_moe_layer_pre(const void* x, int x_dtype, int64_t m, int64_
     set_error("moe layer: buffers must be 16-byte aligned");
     return MXFP4_ERR_VALUE;
   }
-  const LayerPlan p = plan_layer(m, top_k, num_experts, hidden, inter, 2);
+  const LayerPlan p = plan_layer(m, top_k, num_experts, hidden, inter, 2, pre13_b != nullptr);
   if (workspace_bytes < p.total) {
     set_error("moe layer: workspace too small (%lld < %lld)", (long long)workspace_bytes,
               (long long)p.total);
