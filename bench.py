@@ -428,6 +428,24 @@ def soft_op_cases(mx, torch, np):
                                                  eid, npp, True, top_k, False, False,
                                                  {"BLOCK_SIZE_M": bm}, torch.bfloat16),
                               fl, BF16_PEAK_TFLOPS))
+        if cdt == torch.bfloat16:
+            # the same calls with a registered prepacked copy of B (a second
+            # weight tensor, so the rows above keep the checkpoint layout)
+            if not any(c[0].endswith("_registered") for c in cases):
+                wp_r, wsc_r = wp.clone(), wsc.clone()
+                mx.register_prepacked(wp_r, wsc_r)
+            cases.append((f"fused_moe_soft_c{name}_m{m}_registered",
+                          lambda a=a, C=C, tw=tw, ids=ids: mx.fused_moe_mxfp4_soft(
+                              a, wp_r, C, one, ones_e, None, wsc_r, tw, ids, empty, empty, empty,
+                              True, top_k, False, False), fl, peak))
+            if m == 512:
+                srt, eid, npp = mx.make_routing_device(ids, e, 64)
+                cases.append((f"aiter_fused_moe_bm64_m{m}_registered",
+                              lambda a=a, C=C, tw=tw, ids=ids, srt=srt, eid=eid, npp=npp:
+                              mx.fused_moe_mxfp4(a, wp_r, C, one, ones_e, None, wsc_r, tw, ids,
+                                                 srt, eid, npp, True, top_k, False, False,
+                                                 {"BLOCK_SIZE_M": 64}, torch.bfloat16),
+                              fl, BF16_PEAK_TFLOPS))
     return cases
 
 

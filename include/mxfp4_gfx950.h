@@ -210,6 +210,21 @@ int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_str
                    const float* topk_weights, int mul_routed_weight, const int32_t* sorted_ids,
                    const int32_t* expert_ids, const int32_t* num_post_padded, int64_t em,
                    int block_m, int64_t num_valid, int top_k, void* stream);
+/* mxfp4_moe_gemm with a prepacked copy of b / b_mx (mxfp4_prepack_w4a16 of
+ * the same num_experts x n x k weights, 16-byte aligned), which the W4A16
+ * prefill kernels read instead; bitwise the same c.  pre_b = pre_s = NULL is
+ * mxfp4_moe_gemm.  b / b_mx are still required (the decode kernels and the
+ * W4A4 / FP32 paths read them).  The reference has no such argument: it is
+ * what the soft op's and AITER's entries (soft:379, aiter:300) use when the
+ * caller has registered a prepacked copy of B. */
+int mxfp4_moe_gemm_pre(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
+                       const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,
+                       const uint8_t* pre_b, const uint16_t* pre_s, int64_t num_experts,
+                       int64_t n, int64_t k, void* c, int c_dtype, int64_t c_row_stride,
+                       const float* a_scale, const float* b_scale, const float* topk_weights,
+                       int mul_routed_weight, const int32_t* sorted_ids,
+                       const int32_t* expert_ids, const int32_t* num_post_padded, int64_t em,
+                       int block_m, int64_t num_valid, int top_k, void* stream);
 
 /*
  * fused_moe_mxfp4_soft(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale,
@@ -235,6 +250,16 @@ int mxfp4_fused_moe(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_st
                     const float* a_scale, const float* b_scale, const float* topk_weights,
                     int mul_routed_weight, const void* topk_ids, int ids_dtype, int64_t m,
                     int top_k, void* workspace, int64_t workspace_bytes, void* stream);
+/* mxfp4_fused_moe with a prepacked copy of b / b_mx, as mxfp4_moe_gemm_pre
+ * (bitwise the same c; with the copy the routing blocks follow the MoE
+ * layer's 16 / 32 / 64-row rule, which the workspace size covers). */
+int mxfp4_fused_moe_pre(const void* a, int a_dtype, int64_t a_rows, int64_t a_row_stride,
+                        const uint8_t* a_mx, const uint8_t* b, const uint8_t* b_mx,
+                        const uint8_t* pre_b, const uint16_t* pre_s, int64_t num_experts,
+                        int64_t n, int64_t k, void* c, int c_dtype, const float* a_scale,
+                        const float* b_scale, const float* topk_weights, int mul_routed_weight,
+                        const void* topk_ids, int ids_dtype, int64_t m, int top_k,
+                        void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * The vLLM MoE layer, vllm:233-265 (silu only):

@@ -788,10 +788,11 @@ GemmArgs routed_args(const void* a, int64_t a_rows, int64_t a_row_stride, const 
 // 35.1); 48 -> 64 rows 66.2 / 41.3 (128: 76.5 / 47.1); 64 -> 128 rows
 // 80.2 / 52.3 (64: 84.0 / 49.3); 256 -> 128 rows 235.9 / 146.5 (64: 235.8 /
 // 151.0).  The W4A4 and FP32 paths keep the 16 / 32 / 64 rule.
-int soft_block_m(int64_t routes, int64_t num_experts, bool w4a16) {
+int soft_block_m(int64_t routes, int64_t num_experts, bool w4a16, bool prepacked) {
   const double avg = (double)routes / (double)(num_experts > 0 ? num_experts : 1);
   if (avg <= 1.5) return 16;
-  if (!w4a16) return avg <= 32.0 ? 32 : 64;
+  // prepacked weights: the MoE layer's rule (tiles tuned on that layout)
+  if (!w4a16 || prepacked) return avg <= 32.0 ? 32 : 64;
   return avg <= 28.0 ? 32 : (avg <= 56.0 ? 64 : 128);
 }
 
@@ -804,9 +805,9 @@ struct SoftPlan {
   int64_t off_counts, off_sorted, off_experts, off_npp, total;
 };
 
-SoftPlan plan_soft(int64_t routes, int64_t num_experts, bool w4a16) {
+SoftPlan plan_soft(int64_t routes, int64_t num_experts, bool w4a16, bool prepacked) {
   SoftPlan p;
-  p.block_m = soft_block_m(routes, num_experts, w4a16);
+  p.block_m = soft_block_m(routes, num_experts, w4a16, prepacked);
   p.zero_c = num_experts + 1 > kMaxExperts;
   p.align_experts = (int)(p.zero_c ? num_experts : num_experts + 1);
   p.drop_to = p.zero_c ? -1 : (int)num_experts;
@@ -819,6 +820,17 @@ SoftPlan plan_soft(int64_t routes, int64_t num_experts, bool w4a16) {
   p.off_npp = off; off = round_up(off + 4, 256);
   p.total = off;
   return p;
+}
+
+// The prepacked copy (prepack.hip) of the GEMM's experts x n x k weights,
+// read by the W4A16 prefill kernels instead of b / bs (bitwise the same
+// results); null pointers: none.
+void set_prepacked(GemmArgs& g, const uint8_t* pre_b, const uint16_t* pre_s, int64_t n,
+                   int64_t k) {
+  g.pre_b = pre_b;
+  g.pre_s = pre_s;
+  g.pre_b_e = prepacked_nibble_bytes(n, k);
+  g.pre_s_e = prepacked_scale_bytes(n, k);
 }
 
 // Zero `bytes` bytes at p (16-byte aligned; bytes % 2 == 0): a fill kernel,
@@ -844,14 +856,33 @@ extern "C" int mxfp4_moe_gemm(const void* a, int a_dtype, int64_t a_rows, int64_
                               const int32_t* sorted_ids, const int32_t* expert_ids,
                               const int32_t* num_post_padded, int64_t em, int block_m,
                               int64_t num_valid, int top_k, void* stream) {
+  return mxfp4_moe_gemm_pre(a, a_dtype, a_rows, a_row_stride, a_mx, b, b_mx, nullptr, nullptr,
+                            num_experts, n, k, c, c_dtype, c_row_stride, a_scale, b_scale,
+                            topk_weights, mul_routed_weight, sorted_ids, expert_ids,
+                            num_post_padded, em, block_m, num_valid, top_k, stream);
+}
+
+extern "C" int mxfp4_moe_gemm_pre(const void* a, int a_dtype, int64_t a_rows,
+                                  int64_t a_row_stride, const uint8_t* a_mx, const uint8_t* b,
+                                  const uint8_t* b_mx, const uint8_t* pre_b, const uint16_t* pre_s,
+                                  int64_t num_experts, int64_t n, int64_t k, void* c, int c_dtype,
+                                  int64_t c_row_stride, const float* a_scale, const float* b_scale,
+                                  const float* topk_weights, int mul_routed_weight,
+                                  const int32_t* sorted_ids, const int32_t* expert_ids,
+                                  const int32_t* num_post_padded, int64_t em, int block_m,
+                                  int64_t num_valid, int top_k, void* stream) {
   int rc = check_routed_args(a, a_dtype, a_row_stride, a_mx, b, num_experts, n, k, c_dtype, top_k,
                              block_m, em);
   if (rc) return rc;
+  if ((pre_b == nullptr) != (pre_s == nullptr)) {
+    set_error("moe gemm: the prepacked nibbles and scales come together");
+    return MXFP4_ERR_VALUE;
+  }
   if (em == 0) return MXFP4_OK;
-  const GemmArgs g = routed_args(a, a_rows, a_row_stride, a_mx, b, b_mx, num_experts, n, k, c,
-                                 c_row_stride, a_scale, b_scale, topk_weights, mul_routed_weight,
-                                 sorted_ids, expert_ids, num_post_padded, em, block_m, num_valid,
-                                 top_k);
+  GemmArgs g = routed_args(a, a_rows, a_row_stride, a_mx, b, b_mx, num_experts, n, k, c,
+                           c_row_stride, a_scale, b_scale, topk_weights, mul_routed_weight,
+                           sorted_ids, expert_ids, num_post_padded, em, block_m, num_valid, top_k);
+  set_prepacked(g, pre_b, pre_s, n, k);
   return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, static_cast<hipStream_t>(stream));
 }
 
@@ -865,7 +896,10 @@ extern "C" int mxfp4_fused_moe_workspace_size(int64_t m, int top_k, int64_t num_
   }
   const bool w4a16 = (a_dtype == MXFP4_DT_BF16 || a_dtype == MXFP4_DT_F16) &&
                      c_dtype != MXFP4_DT_F32;
-  *bytes = plan_soft(m * top_k, num_experts, w4a16).total;
+  // either layout's plan fits (the caller may pass a prepacked copy)
+  const int64_t x = plan_soft(m * top_k, num_experts, w4a16, false).total;
+  const int64_t y = plan_soft(m * top_k, num_experts, w4a16, true).total;
+  *bytes = x > y ? x : y;
   return MXFP4_OK;
 }
 
@@ -876,9 +910,27 @@ extern "C" int mxfp4_fused_moe(const void* a, int a_dtype, int64_t a_rows, int64
                                const float* topk_weights, int mul_routed_weight,
                                const void* topk_ids, int ids_dtype, int64_t m, int top_k,
                                void* workspace, int64_t workspace_bytes, void* stream) {
+  return mxfp4_fused_moe_pre(a, a_dtype, a_rows, a_row_stride, a_mx, b, b_mx, nullptr, nullptr,
+                             num_experts, n, k, c, c_dtype, a_scale, b_scale, topk_weights,
+                             mul_routed_weight, topk_ids, ids_dtype, m, top_k, workspace,
+                             workspace_bytes, stream);
+}
+
+extern "C" int mxfp4_fused_moe_pre(const void* a, int a_dtype, int64_t a_rows,
+                                   int64_t a_row_stride, const uint8_t* a_mx, const uint8_t* b,
+                                   const uint8_t* b_mx, const uint8_t* pre_b, const uint16_t* pre_s,
+                                   int64_t num_experts, int64_t n, int64_t k, void* c, int c_dtype,
+                                   const float* a_scale, const float* b_scale,
+                                   const float* topk_weights, int mul_routed_weight,
+                                   const void* topk_ids, int ids_dtype, int64_t m, int top_k,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
   if (ids_dtype != MXFP4_DT_I32 && ids_dtype != MXFP4_DT_I64) {
     set_error("topk_ids must be int32 or int64");
     return MXFP4_ERR_TYPE;
+  }
+  if ((pre_b == nullptr) != (pre_s == nullptr)) {
+    set_error("fused moe: the prepacked nibbles and scales come together");
+    return MXFP4_ERR_VALUE;
   }
   if (m < 0 || m * (int64_t)(top_k > 0 ? top_k : 1) > (int64_t)0x3FFFFFFF ||
       num_experts > kMaxExperts) {
@@ -889,7 +941,7 @@ extern "C" int mxfp4_fused_moe(const void* a, int a_dtype, int64_t a_rows, int64
   const int64_t routes = m * top_k;
   const bool w4a16 = (a_dtype == MXFP4_DT_BF16 || a_dtype == MXFP4_DT_F16) &&
                      c_dtype != MXFP4_DT_F32;
-  const SoftPlan p = plan_soft(routes, num_experts, w4a16);
+  const SoftPlan p = plan_soft(routes, num_experts, w4a16, w4a16 && pre_b != nullptr);
   int rc = check_routed_args(a, a_dtype, a_row_stride, a_mx, b, num_experts, n, k, c_dtype, top_k,
                              p.block_m, p.max_sorted);
   if (rc) return rc;
@@ -919,9 +971,10 @@ extern "C" int mxfp4_fused_moe(const void* a, int a_dtype, int64_t a_rows, int64
   rc = do_align(topk_ids, ids_dtype, routes, p.align_experts, p.block_m, sorted, experts, npp,
                 counts, p.nchunks, st, p.drop_to);
   if (rc) return rc;
-  const GemmArgs g = routed_args(a, a_rows, a_row_stride, a_mx, b, b_mx, num_experts, n, k, c, n,
-                                 a_scale, b_scale, topk_weights, mul_routed_weight, sorted, experts,
-                                 npp, p.max_sorted, p.block_m, routes, top_k);
+  GemmArgs g = routed_args(a, a_rows, a_row_stride, a_mx, b, b_mx, num_experts, n, k, c, n,
+                           a_scale, b_scale, topk_weights, mul_routed_weight, sorted, experts, npp,
+                           p.max_sorted, p.block_m, routes, top_k);
+  set_prepacked(g, pre_b, pre_s, n, k);
   return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, st);
 }
 

@@ -14,7 +14,9 @@ current stream; no host synchronisation, no fallback path):
 * ``dynamic_mxfp4_quant`` / ``linear_mxfp4_w4a4`` -- activation quantizer
   and dense W4A4 on the block-scaled FP4 MFMA;
 * ``prepack_w4a16`` -- the fragment-ordered weight copy the prefill GEMMs
-  read when given one (``prepacked=`` / ``prepacked13=``, ``prepacked2=``).
+  read when given one (``prepacked=`` / ``prepacked13=``, ``prepacked2=``);
+  ``register_prepacked`` records one for expert weights, which
+  ``fused_moe_mxfp4_soft`` / ``fused_moe_mxfp4`` then find by address.
 
 ``mxfp4_amd.vllm_adapter.install()`` points vLLM's compressed-tensors MXFP4
 schemes at these operators (integration/vllm/vllm_mxfp4_gfx936.py).
@@ -30,7 +32,13 @@ from .moe_op_mxfp4_soft import (  # noqa: F401
 from .moe_op_mxfp4 import fused_moe_mxfp4  # noqa: F401
 from .moe_layer import make_routing, moe_layer, route_topk  # noqa: F401
 from .quant import dynamic_mxfp4_quant, linear_mxfp4_w4a4  # noqa: F401
-from .prepack import PrepackedWeights, prepack_w4a16  # noqa: F401
+from .prepack import (  # noqa: F401
+    PrepackedWeights,
+    lookup_prepacked,
+    prepack_w4a16,
+    register_prepacked,
+    unregister_prepacked,
+)
 from . import _lib  # noqa: F401
 
 __all__ = [
@@ -46,4 +54,7 @@ __all__ = [
     "linear_mxfp4_w4a4",
     "prepack_w4a16",
     "PrepackedWeights",
+    "register_prepacked",
+    "unregister_prepacked",
+    "lookup_prepacked",
 ]

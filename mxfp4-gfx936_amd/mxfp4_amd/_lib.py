@@ -51,9 +51,13 @@ SIGNATURES = {
     "mxfp4_moe_route": [_P, _I64, _I, _I64, _I, _I, _P, _P, _I, _P],
     "mxfp4_moe_gemm": [_P, _I, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I, _I64, _P, _P,
                        _P, _I, _P, _P, _P, _I64, _I, _I64, _I, _P],
+    "mxfp4_moe_gemm_pre": [_P, _I, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I,
+                           _I64, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I64, _I, _P],
     "mxfp4_fused_moe_workspace_size": [_I64, _I, _I64, _I, _I, _P],
     "mxfp4_fused_moe": [_P, _I, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _I, _P, _P, _P, _I,
                         _P, _I, _I64, _I, _P, _I64, _P],
+    "mxfp4_fused_moe_pre": [_P, _I, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I,
+                            _P, _P, _P, _I, _P, _I, _I64, _I, _P, _I64, _P],
     "mxfp4_moe_layer_workspace_size": [_I64, _I, _I, _I64, _I64, _P],
     "mxfp4_moe_layer": [_P, _I, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _P, _I, _I, _P, _P,
                         _I64, _P],

@@ -25,6 +25,8 @@ Differences, all explicit: swizzled MX scales raise NotImplementedError
 (the reference kernel marks them TODO, aiter:69-70, 189-205); ``config``
 contributes only BLOCK_SIZE_M (tile shapes are chosen by the library);
 ``compute_type`` must name C's dtype; FP8 A with ``A_mx_scale`` is accepted.
+A prepacked copy of B recorded with ``prepack.register_prepacked`` is read
+by the W4A16 prefill kernels while it is current (bitwise the same C).
 """
 
 from __future__ import annotations
@@ -35,6 +37,7 @@ import torch
 
 from . import _lib
 from .moe_op_mxfp4_soft import _FP8_DTYPES, _moe_gemm_launch, _prepare_moe_operands
+from .prepack import lookup_prepacked
 
 _COMPUTE_NAMES = {
     torch.bfloat16: ("bfloat16", "bf16"),
@@ -113,6 +116,6 @@ def fused_moe_mxfp4(
     out = C if C.is_contiguous() and C.data_ptr() % 16 == 0 else C.contiguous().clone()
     _moe_gemm_launch(act, act_mx, b, b_mx, out.view(num_routes, B.shape[1]), a_scale, b_scale,
                      weights, mul_routed_weight, sorted_ids, experts, npp, block_m, num_routes,
-                     top_k, device)
+                     top_k, device, lookup_prepacked(B, B_mx_scale))
     if out is not C:
         C.copy_(out)

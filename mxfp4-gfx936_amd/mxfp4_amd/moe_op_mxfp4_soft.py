@@ -24,11 +24,12 @@ import torch
 
 try:
     from . import _lib
-    from .prepack import PrepackedWeights, check_prepacked
+    from .prepack import PrepackedWeights, check_prepacked, lookup_prepacked
 except ImportError:  # loaded by file path, outside its package
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     from mxfp4_amd import _lib  # type: ignore[no-redef]
-    from mxfp4_amd.prepack import PrepackedWeights, check_prepacked  # type: ignore[no-redef]
+    from mxfp4_amd.prepack import (  # type: ignore[no-redef]
+        PrepackedWeights, check_prepacked, lookup_prepacked)
 
 # soft:12-29 (OCP E2M1 code -> value; bit 3 is the sign)
 _MXFP4_E2M1_VALUES = (
@@ -226,17 +227,19 @@ def make_routing_device(topk_ids: torch.Tensor, num_experts: int, block_m: int):
 
 def _moe_gemm_launch(A, A_mx_scale, B, B_mx_scale, C2d, A_scale, B_scale, topk_weights,
                      mul_routed_weight, sorted_ids, expert_ids, npp, block_m, num_valid,
-                     top_k, device):
+                     top_k, device, pre=None):
     """Launch the routed grouped GEMM writing rows of the contiguous 2-D view
-    ``C2d`` [routes, N]."""
+    ``C2d`` [routes, N] (``pre``: a current prepacked copy of B, or None)."""
     lib = _lib.load()
     num_experts, n, k = B.shape[0], B.shape[1], B.shape[2] * 2
     a_code = _lib.dtype_code(A.dtype)
     a_row_stride = A.stride(0)
+    pre_b, pre_s = (None, None) if pre is None else (pre.nibbles, pre.scales)
     with _lib.on_device(device):
-        _lib.check(lib.mxfp4_moe_gemm(
+        _lib.check(lib.mxfp4_moe_gemm_pre(
             _lib.ptr(A), a_code, A.shape[0], a_row_stride, _lib.ptr(A_mx_scale), _lib.ptr(B),
-            _lib.ptr(B_mx_scale), num_experts, n, k, _lib.ptr(C2d), _lib.dtype_code(C2d.dtype),
+            _lib.ptr(B_mx_scale), _lib.ptr(pre_b), _lib.ptr(pre_s), num_experts, n, k,
+            _lib.ptr(C2d), _lib.dtype_code(C2d.dtype),
             C2d.stride(0), _lib.ptr(A_scale), _lib.ptr(B_scale), _lib.ptr(topk_weights),
             1 if mul_routed_weight else 0, _lib.ptr(sorted_ids), _lib.ptr(expert_ids),
             _lib.ptr(npp), sorted_ids.numel(), block_m, num_valid, top_k,
@@ -353,7 +356,9 @@ def fused_moe_mxfp4_soft(
     as its Triton kernel does (soft:428-464, 100-115), C is zero-filled and
     the grouped GEMM runs over the caller's ``sorted_token_ids`` /
     ``expert_ids`` / ``num_tokens_post_padded`` (expert -1 blocks give
-    zeros; routes the metadata does not name stay zero).
+    zeros; routes the metadata does not name stay zero).  A prepacked copy
+    of B recorded with ``prepack.register_prepacked`` is read instead of B
+    while it is current (bitwise the same C).
     """
     if swizzle_mx_a or swizzle_mx_b:
         raise NotImplementedError("the gfx936 software fallback does not support swizzled scales")
@@ -405,10 +410,13 @@ def fused_moe_mxfp4_soft(
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     out = C if C.is_contiguous() and C.data_ptr() % 16 == 0 else torch.empty(
         C.shape, dtype=C.dtype, device=device)
+    pre = lookup_prepacked(B, B_mx_scale)
+    pre_b, pre_s = (None, None) if pre is None else (pre.nibbles, pre.scales)
     with _lib.on_device(device):
-        _lib.check(lib.mxfp4_fused_moe(
+        _lib.check(lib.mxfp4_fused_moe_pre(
             _lib.ptr(act), a_code, act.shape[0], act.stride(0), _lib.ptr(act_mx), _lib.ptr(b),
-            _lib.ptr(b_mx), num_experts, n, k, _lib.ptr(out), c_code, _lib.ptr(a_scale),
+            _lib.ptr(b_mx), _lib.ptr(pre_b), _lib.ptr(pre_s), num_experts, n, k, _lib.ptr(out),
+            c_code, _lib.ptr(a_scale),
             _lib.ptr(b_scale), _lib.ptr(weights), 1 if mul_routed_weight else 0, _lib.ptr(ids),
             _lib.dtype_code(ids.dtype), m, top_k, _lib.ptr(ws), ws_bytes,
             _lib.stream_of(device)))
@@ -455,6 +463,6 @@ def _fused_moe_caller_metadata(A, B, C, A_scale, B_scale, B_mx_scale, topk_weigh
         C.shape, dtype=C.dtype, device=device)
     _moe_gemm_launch(act, act_mx, b, b_mx, out.view(num_routes, B.shape[1]), a_scale, b_scale,
                      weights, mul_routed_weight, sorted_ids, experts, npp, block_m, num_routes,
-                     top_k, device)
+                     top_k, device, lookup_prepacked(B, B_mx_scale))
     if out is not C:
         C.copy_(out)

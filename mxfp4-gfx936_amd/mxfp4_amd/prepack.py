@@ -24,11 +24,22 @@ weights, and the vLLM hooks prepack such weights again before the call.
 Writes through ``param.data`` are not versioned by PyTorch (``.data`` is a
 new tensor with its own counter) and are not seen: prepack again after them
 (``vllm_adapter.refresh_prepacked(layer)`` for a vLLM layer).
+
+The routed operators keep the reference's signatures (soft:379-396,
+aiter:367-386), which have no place for a copy.  ``register_prepacked(B,
+B_mx_scale)`` prepacks expert weights once and records the copy against
+those tensors; ``fused_moe_mxfp4_soft`` and ``fused_moe_mxfp4`` then look
+it up by B's address and use it while it is current (same tensors, same
+shapes, no in-place write since), with bitwise the same C.  A stale entry is
+dropped at lookup and the call reads the checkpoint layout; an entry also
+goes when the registered weight tensor is freed.
 """
 
 from __future__ import annotations
 
 import ctypes
+import threading
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -128,3 +139,70 @@ def check_prepacked(pre: PrepackedWeights | None, experts: int, rows: int, k: in
             f"{what}: prepacked copy is stale: it was made from other weight tensors, or "
             f"they were written in place since; call prepack_w4a16 again")
     return pre
+
+
+# data_ptr of the registered packed weights -> (copy, weak reference to that
+# tensor); the reference's callback removes the entry when the tensor is
+# freed, so a later tensor at the same address never meets the old copy
+_REGISTRY: dict = {}
+_REGISTRY_LOCK = threading.Lock()
+
+
+def register_prepacked(packed: torch.Tensor, block_scales: torch.Tensor,
+                       prepacked: PrepackedWeights | None = None) -> PrepackedWeights:
+    """Record a prepacked copy of expert weights ``packed`` [E, N, K/2] /
+    ``block_scales`` [E, N, K/32] for the routed operators (made here with
+    ``prepack_w4a16`` unless ``prepacked`` is given, which must have been made
+    from these tensors).  Registering the same tensor again replaces the
+    copy.  Returns the registered copy."""
+    if packed.ndim != 3 or block_scales.ndim != 3:
+        raise ValueError("register_prepacked takes expert weights [E, N, K/2] / [E, N, K/32]")
+    experts, rows, k = packed.shape[0], packed.shape[1], packed.shape[2] * 2
+    if prepacked is None:
+        prepacked = prepack_w4a16(packed, block_scales)
+    check_prepacked(prepacked, experts, rows, k, packed.device, "register_prepacked", packed,
+                    block_scales)
+    key = packed.data_ptr()
+
+    def _drop(ref, key=key):
+        with _REGISTRY_LOCK:
+            entry = _REGISTRY.get(key)
+            if entry is not None and entry[1] is ref:
+                del _REGISTRY[key]
+
+    with _REGISTRY_LOCK:
+        _REGISTRY[key] = (prepacked, weakref.ref(packed, _drop))
+    return prepacked
+
+
+def unregister_prepacked(packed: torch.Tensor) -> None:
+    """Forget the copy registered for ``packed`` (no error if there is none)."""
+    with _REGISTRY_LOCK:
+        _REGISTRY.pop(packed.data_ptr(), None)
+
+
+def lookup_prepacked(packed: torch.Tensor, block_scales: torch.Tensor) -> PrepackedWeights | None:
+    """The registered copy of (packed, block_scales) when it is current, else
+    None.  An entry whose registered weight tensor was written in place since
+    is removed (version counters only grow, so it cannot become current)."""
+    if not _REGISTRY or packed.ndim != 3:
+        return None
+    key = packed.data_ptr()
+    with _REGISTRY_LOCK:
+        entry = _REGISTRY.get(key)
+    registered = None if entry is None else entry[1]()
+    if registered is None:
+        return None
+    pre = entry[0]
+    experts, rows, k = packed.shape[0], packed.shape[1], packed.shape[2] * 2
+    if not pre.matches(experts, rows, k, packed.device):
+        return None
+    if pre.is_current(packed, block_scales):
+        return pre
+    if _source_of(registered) != pre.source[0]:
+        # judged on the registered tensor's own counter: another tensor over
+        # the same memory (param.data) counts writes separately
+        with _REGISTRY_LOCK:
+            if _REGISTRY.get(key) is entry:
+                del _REGISTRY[key]
+    return None

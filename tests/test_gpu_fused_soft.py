@@ -178,3 +178,68 @@ def test_soft_op_triton_backend_uses_caller_metadata(block_m, monkeypatch):
     assert not np.isnan(out).any()
     assert np.all(out.reshape(m * top_k, n)[left_out] == 0)
     assert_parity(out, oracle, what=f"triton backend block {block_m}")
+
+
+# routes per expert 16 (32-row blocks either way) and 128 (128-row blocks on
+# the checkpoint layout, 64 with a copy); N 200 leaves a ragged 16-row group
+@pytest.mark.parametrize("m,e,top_k,n", [(64, 16, 4, 192), (512, 16, 4, 200)],
+                         ids=["blk32", "blk128"])
+@pytest.mark.parametrize("c_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_registered_copy_is_bitwise_the_checkpoint_result(m, e, top_k, n, c_dtype, monkeypatch):
+    # a registered prepacked copy of B is read by the soft op (device
+    # routing), its triton-backend value (caller metadata) and AITER's entry;
+    # each C equals the unregistered call's bit for bit
+    from mxfp4_amd import prepack as P
+    print(f"registered copy m={m} e={e} n={n} {c_dtype}", flush=True)
+    rng = np.random.default_rng(3 * m + n)
+    k = 512
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    B, Bs = cuda(wp), cuda(ws)
+    A = cuda(rand_act(m + 77, (m, k))).to(c_dtype)
+    w, ids = _route_with_dropped(m, e, top_k, 4000 + m, 11)
+    w, ids = cuda(w), cuda(ids)
+    a_scale = torch.tensor([0.75], device="cuda")
+    b_scale = torch.linspace(0.5, 1.5, e, device="cuda")
+    srt, exp_, npp = (cuda(t) for t in O.make_routing(ids.cpu().numpy(), block_m=64,
+                                                         num_experts=e))
+
+    def soft():
+        C = torch.full((m, top_k, n), float("nan"), dtype=c_dtype, device="cuda")
+        mx.fused_moe_mxfp4_soft(A, B, C, a_scale, b_scale, None, Bs, w, ids, _empty(), _empty(),
+                                _empty(), True, top_k, False, False)
+        return C
+
+    def triton():
+        monkeypatch.setenv("MXFP4_GFX936_BACKEND", "triton")
+        C = torch.full((m, top_k, n), float("nan"), dtype=c_dtype, device="cuda")
+        mx.fused_moe_mxfp4_soft(A, B, C, a_scale, b_scale, None, Bs, w, ids, srt, exp_, npp,
+                                True, top_k, False, False)
+        monkeypatch.delenv("MXFP4_GFX936_BACKEND")
+        return C
+
+    def aiter():
+        C = torch.full((m, top_k, n), 3.0, dtype=c_dtype, device="cuda")
+        mx.fused_moe_mxfp4(A, B, C, a_scale, b_scale, None, Bs, w, ids, srt, exp_, npp, True,
+                           top_k, False, False, {"BLOCK_SIZE_M": 64}, c_dtype)
+        return C
+
+    plain = [f() for f in (soft, triton, aiter)]
+    pre = P.register_prepacked(B, Bs)
+    try:
+        assert P.lookup_prepacked(B, Bs) is pre
+        fast = [f() for f in (soft, triton, aiter)]
+        torch.cuda.synchronize()
+        for name, x, y in zip(("soft", "triton", "aiter"), plain, fast):
+            assert torch.equal(x, y), name
+            assert not torch.isnan(x).any(), name
+        # an in-place weight update makes the copy stale: the calls read the
+        # new checkpoint weights (and the entry is dropped)
+        wp2, _ = rand_mxfp4(rng, (e, n), k)
+        B.copy_(cuda(wp2))
+        after = soft()
+        assert P.lookup_prepacked(B, Bs) is None
+        P.unregister_prepacked(B)
+        assert torch.equal(after, soft())
+        assert not torch.equal(after, plain[0])
+    finally:
+        P.unregister_prepacked(B)

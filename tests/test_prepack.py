@@ -135,3 +135,72 @@ def test_vllm_hooks_prepack_again_after_an_update(monkeypatch):
     assert len(made) == 3
     V.refresh_prepacked(layer)
     assert len(made) == 4
+
+
+def test_registry_serves_current_copies_only():
+    # register / lookup / unregister with a hand-built copy of CPU tensors
+    # (the rule is host logic; the GPU tests run the operators through it)
+    import gc
+
+    from mxfp4_amd.prepack import (_REGISTRY, _source_of, lookup_prepacked, register_prepacked,
+                                   unregister_prepacked)
+    w = torch.zeros((2, 16, 32), dtype=torch.uint8)
+    s = torch.zeros((2, 16, 2), dtype=torch.uint8)
+
+    def copy_of(w, s):
+        return PrepackedWeights(torch.zeros(1), torch.zeros(1), 2, 16, 64,
+                                (_source_of(w), _source_of(s)))
+    pre = register_prepacked(w, s, copy_of(w, s))
+    assert lookup_prepacked(w, s) is pre
+    assert lookup_prepacked(w.view(2, 16, 32), s) is pre
+    assert lookup_prepacked(w.clone(), s) is None           # other weights
+    assert lookup_prepacked(w, s.clone()) is None           # other scales: not served ...
+    assert lookup_prepacked(w, s) is pre                    # ... but not dropped either
+    assert lookup_prepacked(w[:1], s[:1]) is None           # another shape at the address
+    with pytest.raises(ValueError, match="stale"):
+        register_prepacked(w.clone(), s, pre)                # a copy of other tensors
+    with pytest.raises(ValueError, match="prepacked copy is for"):
+        register_prepacked(w[:, :8], s[:, :8], pre)
+    w[1, 3, 0] = 7                                          # in-place write: stale for good
+    assert lookup_prepacked(w, s) is None
+    assert w.data_ptr() not in _REGISTRY
+    pre2 = register_prepacked(w, s, copy_of(w, s))
+    assert lookup_prepacked(w, s) is pre2
+    unregister_prepacked(w)
+    assert lookup_prepacked(w, s) is None
+    unregister_prepacked(w)                                 # no error when absent
+    # the entry goes with the registered tensor, so memory reused at that
+    # address never meets the old copy
+    w3 = torch.zeros((2, 16, 32), dtype=torch.uint8)
+    register_prepacked(w3, s, copy_of(w3, s))
+    key = w3.data_ptr()
+    del w3
+    gc.collect()
+    assert key not in _REGISTRY
+    with pytest.raises(ValueError, match=r"\[E, N, K/2\]"):
+        register_prepacked(w[0], s[0], pre)
+
+
+def test_prepacked_entry_points_refuse_half_a_copy():
+    # the C-ABI _pre entry points need both halves of the copy; the check
+    # runs before anything touches the device
+    import ctypes
+
+    from mxfp4_amd import _lib
+    lib = _lib.load()
+    null, fake = ctypes.c_void_p(), ctypes.c_void_p(4096)
+    rc = lib.mxfp4_moe_gemm_pre(null, _lib.DT_BF16, 1, 128, null, null, null, fake, null, 4, 64,
+                                128, null, _lib.DT_BF16, 64, null, null, null, 0, null, null, null,
+                                16, 16, 2, 2, null)
+    assert rc == _lib.ERR_VALUE and "come together" in lib.mxfp4_last_error().decode()
+    rc = lib.mxfp4_fused_moe_pre(null, _lib.DT_BF16, 1, 128, null, null, null, null, fake, 4, 64,
+                                 128, null, _lib.DT_BF16, null, null, null, 0, null, _lib.DT_I32,
+                                 1, 2, null, 0, null)
+    assert rc == _lib.ERR_VALUE and "come together" in lib.mxfp4_last_error().decode()
+    # the workspace covers either layout's routing blocks
+    a, b = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.mxfp4_fused_moe_workspace_size(512, 4, 16, _lib.DT_BF16, _lib.DT_BF16,
+                                              ctypes.byref(a)) == 0
+    assert lib.mxfp4_fused_moe_workspace_size(512, 4, 16, _lib.DT_F32, _lib.DT_F32,
+                                              ctypes.byref(b)) == 0
+    assert a.value > 0 and b.value > 0
