@@ -787,12 +787,31 @@ GemmArgs routed_args(const void* a, int64_t a_rows, int64_t a_row_stride, const 
 // (64 rows: 54.6 / 33.2); 32 -> 64 rows 59.0 / 35.9 (32 rows: 67.7 /
 // 35.1); 48 -> 64 rows 66.2 / 41.3 (128: 76.5 / 47.1); 64 -> 128 rows
 // 80.2 / 52.3 (64: 84.0 / 49.3); 256 -> 128 rows 235.9 / 146.5 (64: 235.8 /
-// 151.0).  The W4A4 and FP32 paths keep the 16 / 32 / 64 rule.
-int soft_block_m(int64_t routes, int64_t num_experts, bool w4a16, bool prepacked) {
+// 151.0).  The W4A4 path keeps the 16 / 32 / 64 rule.  The FP32 path
+// (f32_pipe, MFMA bound, skipping row blocks of padding only): 16 rows up to
+// 8 routes per expert, else 32 (AITER's entry on the same routes, K=2048
+// N=1536: 4 routes per expert 153.6 / 163.9 / 221.7 us for 16 / 32 / 64;
+// 32: 366.0 / 337.7 / 374.2; 128: 1219 / 1048 / 1107).
+enum SoftPath {
+  SOFT_W4A16,      // bf16 / fp16 A and C, checkpoint-layout weights
+  SOFT_W4A16_PRE,  // the same with a prepacked copy
+  SOFT_SCALED,     // packed MXFP4 / FP8 A on the block-scaled MFMA
+  SOFT_F32,        // C in FP32
+};
+
+SoftPath soft_path(int a_dtype, int c_dtype, bool prepacked) {
+  if (a_dtype == MXFP4_DT_U8 || a_dtype == MXFP4_DT_F8E4M3 || a_dtype == MXFP4_DT_F8E5M2)
+    return SOFT_SCALED;
+  if (c_dtype == MXFP4_DT_F32) return SOFT_F32;
+  return prepacked ? SOFT_W4A16_PRE : SOFT_W4A16;
+}
+
+int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path) {
   const double avg = (double)routes / (double)(num_experts > 0 ? num_experts : 1);
   if (avg <= 1.5) return 16;
+  if (path == SOFT_F32) return avg <= 8.0 ? 16 : 32;
   // prepacked weights: the MoE layer's rule (tiles tuned on that layout)
-  if (!w4a16 || prepacked) return avg <= 32.0 ? 32 : 64;
+  if (path != SOFT_W4A16) return avg <= 32.0 ? 32 : 64;
   return avg <= 28.0 ? 32 : (avg <= 56.0 ? 64 : 128);
 }
 
@@ -805,9 +824,9 @@ struct SoftPlan {
   int64_t off_counts, off_sorted, off_experts, off_npp, total;
 };
 
-SoftPlan plan_soft(int64_t routes, int64_t num_experts, bool w4a16, bool prepacked) {
+SoftPlan plan_soft(int64_t routes, int64_t num_experts, SoftPath path) {
   SoftPlan p;
-  p.block_m = soft_block_m(routes, num_experts, w4a16, prepacked);
+  p.block_m = soft_block_m(routes, num_experts, path);
   p.zero_c = num_experts + 1 > kMaxExperts;
   p.align_experts = (int)(p.zero_c ? num_experts : num_experts + 1);
   p.drop_to = p.zero_c ? -1 : (int)num_experts;
@@ -894,11 +913,9 @@ extern "C" int mxfp4_fused_moe_workspace_size(int64_t m, int top_k, int64_t num_
               (long long)num_experts);
     return MXFP4_ERR_VALUE;
   }
-  const bool w4a16 = (a_dtype == MXFP4_DT_BF16 || a_dtype == MXFP4_DT_F16) &&
-                     c_dtype != MXFP4_DT_F32;
   // either layout's plan fits (the caller may pass a prepacked copy)
-  const int64_t x = plan_soft(m * top_k, num_experts, w4a16, false).total;
-  const int64_t y = plan_soft(m * top_k, num_experts, w4a16, true).total;
+  const int64_t x = plan_soft(m * top_k, num_experts, soft_path(a_dtype, c_dtype, false)).total;
+  const int64_t y = plan_soft(m * top_k, num_experts, soft_path(a_dtype, c_dtype, true)).total;
   *bytes = x > y ? x : y;
   return MXFP4_OK;
 }
@@ -939,9 +956,7 @@ extern "C" int mxfp4_fused_moe_pre(const void* a, int a_dtype, int64_t a_rows,
     return MXFP4_ERR_VALUE;
   }
   const int64_t routes = m * top_k;
-  const bool w4a16 = (a_dtype == MXFP4_DT_BF16 || a_dtype == MXFP4_DT_F16) &&
-                     c_dtype != MXFP4_DT_F32;
-  const SoftPlan p = plan_soft(routes, num_experts, w4a16, w4a16 && pre_b != nullptr);
+  const SoftPlan p = plan_soft(routes, num_experts, soft_path(a_dtype, c_dtype, pre_b != nullptr));
   int rc = check_routed_args(a, a_dtype, a_row_stride, a_mx, b, num_experts, n, k, c_dtype, top_k,
                              p.block_m, p.max_sorted);
   if (rc) return rc;
