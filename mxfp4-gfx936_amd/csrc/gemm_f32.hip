@@ -12,11 +12,12 @@
 // Tile BM x 128 (BM = 16, 32 or 64: routed tiles must not straddle an
 // expert block of block_m rows), 4 waves side by side on columns, each wave
 // all BM rows x 32 columns (BM/16 x 2 MFMA blocks).  K runs in 32-deep
-// stages through two LDS buffers: the global loads of stage s + 1 (16-byte
-// activation chunks of the gathered rows; 8 packed weight bytes and the
-// stage's E8M0 byte per thread) are in flight while the MFMAs of stage s
-// run, then land in the other buffer (activations widened to FP32, weights
-// decoded to FP32), one barrier per stage.  LDS rows are 36 floats (144
+// stages through two LDS buffers.  During stage s the global loads of
+// stage s + 2 go out (16-byte activation chunks of the gathered rows; 8
+// packed weight bytes and the stage's E8M0 byte per thread, into one of two
+// register sets), the MFMAs of stage s run, and stage s + 1 (loaded during
+// stage s - 1) lands in the other buffer (activations widened to FP32,
+// weights decoded to FP32); one barrier per stage.  LDS rows are 36 floats (144
 // bytes), so the 16-byte fragment reads of 8 consecutive rows fall in 8
 // different bank groups.
 //
