@@ -1066,7 +1066,10 @@ int pf_choose(const GemmArgs& g, int epi) {
     const double f320 = epi == EPI_STORE ? fill(320) : 0.0;
     if (f320 >= 0.8 && f320 >= f256) return PF_128x320;
     if (f256 >= 0.8) return PF_128x256;
-    if (tiles(128, 128) >= 512) return PF_128x128;
+    // dense grids from 448 tiles, 7/8 of one round at two per CU (qkv K=2048
+    // N=5120 M=1536, graph replays: 30.4 vs 33.7 us on 64 x 128; M=1024, 320
+    // tiles: 27.7 vs 26.2)
+    if (tiles(128, 128) >= (routed ? 512 : 448)) return PF_128x128;
   }
   // Routed 64-row blocks (MoE prefill at ~300-1300 tokens): 64 x 256 tiles,
   // which stream each expert's weights in half as many tiles (MoE layer,
@@ -1098,11 +1101,13 @@ int pf_choose(const GemmArgs& g, int epi) {
     if (cus > 0 && t256 > 4 * cus) return epi == EPI_SILU_MUL ? PF_32x384 : PF_32x512;
     return PF_32x256;
   }
-  // 64-row waves halve the decode work per MFMA of 32-row ones; they win
-  // from ~200 tiles (qkv K=2048 N=5120, steady clocks: M=370 18.1 -> 16.8
-  // us, M=512 23.8 -> 20.7 us; M=256, 160 tiles, stays with 32 rows: 15.6
-  // vs 17.8 us)
-  if (allowed(64) && tiles(64, 128) >= 200) return PF_64x128;
+  // 64-row waves halve the decode work per MFMA of 32-row ones, and win
+  // once their tiles fill the chip: from 384 of them (graph replays over
+  // cold weight copies, prepacked, 64 x 128 vs 32 x 128 tiles: qkv K=2048
+  // N=5120 M=370 (240 tiles) 15.75 vs 14.65 us, M=512 (320) 18.51 vs 17.47,
+  // M=640 (400) 18.93 vs 21.51; o_proj K=4096 N=2048 M=1024 (256) 26.80 vs
+  // 24.70, M=1536 (384) 31.90 vs 32.23, M=2048 (512) 35.32 vs 40.23)
+  if (allowed(64) && tiles(64, 128) >= 384) return PF_64x128;
   return PF_32x128;
 }
 
@@ -1177,9 +1182,12 @@ SplitPlan splitk_plan(int64_t m, int64_t k, int64_t n) {
   // -> split: o_proj K=4096 N=2048 M=128 / 200 / 256 / 370: 22.4 / 22.5 /
   // 22.5 / 22.6 -> 12.6 / 15.6 / 16.8 / 20.3 us; M=130 K=8192 N=640: 43.5
   // -> 13.4 us; M=64 K=2048 N=1536: 13.1 -> 10.4 us).
+  // Long K (>= 64 stages) splits while the 32-row tiles number under 384
+  // (o_proj M=512, 256 tiles: 2 slices 20.4-21.0 vs 22.7 us; M=640: 22.8 vs
+  // 23.9; M=768, 384 tiles: 24.0 vs 24.0).
   SplitPlan p{m <= 256 ? PF_32x128 : PF_64x128, 1};
   const int64_t tiles32 = ((m + 31) / 32) * ((n + 127) / 128);
-  if (tiles32 >= 256 || (k < 4096 && tiles32 >= 64)) return p;
+  if (tiles32 >= 384 || (k < 4096 && tiles32 >= 64)) return p;
   const int bm = m <= 256 ? 32 : 64;
   const int64_t tiles = ((m + bm - 1) / bm) * ((n + 127) / 128);
   const int64_t nk = k / 64;
