@@ -1,7 +1,7 @@
 """GPU: the operators inside a captured HIP graph.  The library synchronises
-nothing and records no memset (only kernels), so the router, the MoE layer
-and the dense linear can be captured once and replayed with new inputs
-copied in place.  Every replay must equal eager calls on the same inputs
+nothing and records no memset (only kernels), so the router, the MoE layer,
+the dense linear, the soft op and AITER's entry can be captured once and
+replayed with new inputs copied in place.  Every replay must equal eager calls on the same inputs
 bitwise (the kernels are deterministic), with the program's own eager work
 and synchronisations between replays."""
 
@@ -69,3 +69,59 @@ def test_graph_replays_equal_eager(m, weights):
         # eager work between replays that reuses freed memory
         torch.empty((m, 4096), device="cuda").fill_(7.0)
         torch.cuda.synchronize()
+
+
+# the soft op (device routing + routed GEMM in one library call) on plain
+# weights, on a registered prepacked copy, with C in FP32; and AITER's entry
+# on metadata the device builds inside the same graph
+@pytest.mark.parametrize("case", ["soft_bf16", "soft_registered", "soft_f32", "aiter"])
+def test_graph_soft_op_replays_equal_eager(case, weights):
+    from mxfp4_amd import prepack as P
+    w13, s13 = weights[0], weights[1]
+    if case == "soft_registered":
+        w13, s13 = w13.clone(), s13.clone()
+        P.register_prepacked(w13, s13)
+    m, top_k, e, n = (64 if case == "soft_f32" else 512), 8, 128, 1536
+    c_dtype = torch.float32 if case == "soft_f32" else torch.bfloat16
+    x = cuda(rand_act(60, (m, 2048)))
+    logits = _logits(m, 61)
+    one, ones_e, empty = (torch.ones(1, device="cuda"), torch.ones(e, device="cuda"),
+                          torch.empty(0, device="cuda"))
+
+    def step():
+        w, ids = mx.route_topk(logits, top_k)
+        C = torch.full((m, top_k, n), 5.0, dtype=c_dtype, device="cuda")
+        if case == "aiter":
+            srt, eid, npp = mx.make_routing_device(ids, e, 64)
+            mx.fused_moe_mxfp4(x, w13, C, one, ones_e, None, s13, w, ids, srt, eid, npp, True,
+                               top_k, False, False, {"BLOCK_SIZE_M": 64}, c_dtype)
+        else:
+            mx.fused_moe_mxfp4_soft(x, w13, C, one, ones_e, None, s13, w, ids, empty, empty,
+                                    empty, True, top_k, False, False)
+        return C
+
+    try:
+        step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                captured = step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            print(f"graph {case} replay {rep}", flush=True)
+            x.copy_(cuda(rand_act(70 + rep, (m, 2048))))
+            logits.copy_(_logits(m, 80 + rep))
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = step()
+            torch.cuda.synchronize()
+            assert torch.equal(captured, eager), f"replay {rep} differs from the eager call"
+            assert torch.isfinite(captured).all()
+            torch.empty((m, 4096), device="cuda").fill_(7.0)
+            torch.cuda.synchronize()
+    finally:
+        P.unregister_prepacked(w13)
