@@ -150,7 +150,9 @@ def linear_mxfp4_soft(
     any other bias is added afterwards with torch's promotion, as the
     reference does (soft:374-375).  ``prepacked`` (keyword only; from
     ``prepack_w4a16(packed, block_scales)``) lets the prefill kernels read
-    the fragment-ordered copy; the result is bitwise the same.
+    the fragment-ordered copy; the result is bitwise the same.  Without it,
+    a current copy recorded with ``prepack.register_prepacked(packed,
+    block_scales)`` is used.
     """
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise TypeError(f"x must be fp16 or bf16, got {x.dtype}")
@@ -174,6 +176,8 @@ def linear_mxfp4_soft(
     n = packed.shape[0]
     pre = check_prepacked(prepacked, 1, n, logical_k, device, "linear_mxfp4_soft", packed,
                           block_scales)
+    if prepacked is None:
+        pre = lookup_prepacked(packed, block_scales)
     x_2d = _lib.aligned(x.reshape(-1, logical_k))
     w = _lib.aligned(packed)
     s = block_scales.contiguous()

@@ -25,12 +25,13 @@ Writes through ``param.data`` are not versioned by PyTorch (``.data`` is a
 new tensor with its own counter) and are not seen: prepack again after them
 (``vllm_adapter.refresh_prepacked(layer)`` for a vLLM layer).
 
-The routed operators keep the reference's signatures (soft:379-396,
-aiter:367-386), which have no place for a copy.  ``register_prepacked(B,
-B_mx_scale)`` prepacks expert weights once and records the copy against
-those tensors; ``fused_moe_mxfp4_soft`` and ``fused_moe_mxfp4`` then look
-it up by B's address and use it while it is current (same tensors, same
-shapes, no in-place write since), with bitwise the same C.  A stale entry is
+The reference's signatures (soft:310-313, 379-396, aiter:367-386) have no
+place for a copy.  ``register_prepacked(weights, scales)`` prepacks dense
+[N, K/2] or expert [E, N, K/2] weights once and records the copy against
+those tensors; ``linear_mxfp4_soft`` (without ``prepacked=``),
+``fused_moe_mxfp4_soft`` and ``fused_moe_mxfp4`` then look it up by the
+weights' address and use it while it is current (same tensors, same shapes,
+no in-place write since), with bitwise the same result.  A stale entry is
 dropped at lookup and the call reads the checkpoint layout; an entry also
 goes when the registered weight tensor is freed.
 """
@@ -150,14 +151,16 @@ _REGISTRY_LOCK = threading.Lock()
 
 def register_prepacked(packed: torch.Tensor, block_scales: torch.Tensor,
                        prepacked: PrepackedWeights | None = None) -> PrepackedWeights:
-    """Record a prepacked copy of expert weights ``packed`` [E, N, K/2] /
-    ``block_scales`` [E, N, K/32] for the routed operators (made here with
+    """Record a prepacked copy of dense weights ``packed`` [N, K/2] /
+    ``block_scales`` [N, K/32] or expert weights [E, N, K/2] / [E, N, K/32]
+    for the operators that take no copy argument (made here with
     ``prepack_w4a16`` unless ``prepacked`` is given, which must have been made
     from these tensors).  Registering the same tensor again replaces the
     copy.  Returns the registered copy."""
-    if packed.ndim != 3 or block_scales.ndim != 3:
-        raise ValueError("register_prepacked takes expert weights [E, N, K/2] / [E, N, K/32]")
-    experts, rows, k = packed.shape[0], packed.shape[1], packed.shape[2] * 2
+    if packed.ndim not in (2, 3) or block_scales.ndim != packed.ndim:
+        raise ValueError("register_prepacked takes weights [N, K/2] / [N, K/32] or "
+                         "[E, N, K/2] / [E, N, K/32]")
+    experts, rows, k = _dims(packed)
     if prepacked is None:
         prepacked = prepack_w4a16(packed, block_scales)
     check_prepacked(prepacked, experts, rows, k, packed.device, "register_prepacked", packed,
@@ -181,11 +184,18 @@ def unregister_prepacked(packed: torch.Tensor) -> None:
         _REGISTRY.pop(packed.data_ptr(), None)
 
 
+def _dims(packed: torch.Tensor):
+    """(experts, rows, K) of dense [N, K/2] or expert [E, N, K/2] weights."""
+    if packed.ndim == 2:
+        return 1, packed.shape[0], packed.shape[1] * 2
+    return packed.shape[0], packed.shape[1], packed.shape[2] * 2
+
+
 def lookup_prepacked(packed: torch.Tensor, block_scales: torch.Tensor) -> PrepackedWeights | None:
     """The registered copy of (packed, block_scales) when it is current, else
     None.  An entry whose registered weight tensor was written in place since
     is removed (version counters only grow, so it cannot become current)."""
-    if not _REGISTRY or packed.ndim != 3:
+    if not _REGISTRY or packed.ndim not in (2, 3):
         return None
     key = packed.data_ptr()
     with _REGISTRY_LOCK:
@@ -194,7 +204,7 @@ def lookup_prepacked(packed: torch.Tensor, block_scales: torch.Tensor) -> Prepac
     if registered is None:
         return None
     pre = entry[0]
-    experts, rows, k = packed.shape[0], packed.shape[1], packed.shape[2] * 2
+    experts, rows, k = _dims(packed)
     if not pre.matches(experts, rows, k, packed.device):
         return None
     if pre.is_current(packed, block_scales):

@@ -138,3 +138,30 @@ def test_stale_prepacked_copy_is_refused_and_the_hooks_refresh():
     va.refresh_prepacked(layer)
     assert torch.equal(va._dense_apply_weights(None, layer, x), y0)
     assert isinstance(layer.weight_packed, Parameter)
+
+
+def test_registered_dense_copy_serves_the_reference_signature():
+    # linear_mxfp4_soft(x, packed, block_scales) -- soft:310's signature, no
+    # copy argument -- reads a copy registered for those tensors: bitwise the
+    # explicit-copy and the checkpoint results; stale after an in-place write
+    from mxfp4_amd import prepack as P
+    rng = np.random.default_rng(411)
+    m, k, n = 1024, 2048, 1536
+    wp, ws = rand_mxfp4(rng, (n,), k)
+    w, s = cuda(wp), cuda(ws)
+    x = cuda(rand_act(412, (m, k)))
+    plain = mx.linear_mxfp4_soft(x, w, s)
+    pre = P.register_prepacked(w, s)
+    try:
+        assert P.lookup_prepacked(w, s) is pre
+        assert torch.equal(mx.linear_mxfp4_soft(x, w, s), plain)
+        assert torch.equal(mx.linear_mxfp4_soft(x, w, s, prepacked=pre), plain)
+        w2, _ = rand_mxfp4(rng, (n,), k)
+        w.copy_(cuda(w2))
+        after = mx.linear_mxfp4_soft(x, w, s)
+        assert P.lookup_prepacked(w, s) is None
+        assert not torch.equal(after, plain)
+        P.register_prepacked(w, s)
+        assert torch.equal(mx.linear_mxfp4_soft(x, w, s), after)
+    finally:
+        P.unregister_prepacked(w)

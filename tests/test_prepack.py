@@ -177,8 +177,18 @@ def test_registry_serves_current_copies_only():
     del w3
     gc.collect()
     assert key not in _REGISTRY
-    with pytest.raises(ValueError, match=r"\[E, N, K/2\]"):
-        register_prepacked(w[0], s[0], pre)
+    with pytest.raises(ValueError, match=r"\[N, K/2\]"):
+        register_prepacked(w[0, 0], s[0, 0], pre)
+    # dense weights [N, K/2]: one expert of N rows
+    wd = torch.zeros((16, 32), dtype=torch.uint8)
+    sd = torch.zeros((16, 2), dtype=torch.uint8)
+    pd = PrepackedWeights(torch.zeros(1), torch.zeros(1), 1, 16, 64, (_source_of(wd), _source_of(sd)))
+    assert register_prepacked(wd, sd, pd) is pd
+    assert lookup_prepacked(wd, sd) is pd
+    with pytest.raises(ValueError, match="prepacked copy is for 1 x 16 x 64"):
+        register_prepacked(wd[:8], sd[:8], pd)
+    unregister_prepacked(wd)
+    assert lookup_prepacked(wd, sd) is None
 
 
 def test_prepacked_entry_points_refuse_half_a_copy():
