@@ -243,3 +243,24 @@ def test_registered_copy_is_bitwise_the_checkpoint_result(m, e, top_k, n, c_dtyp
         assert not torch.equal(after, plain[0])
     finally:
         P.unregister_prepacked(B)
+
+
+# the FP32 path's 32-deep stages run in pairs with two register sets: one
+# stage (K=32), an odd count (K=96, 160) and an even one (K=256); ragged N;
+# 16- and 32-row routing blocks (4 and 40 routes per expert)
+@pytest.mark.parametrize("k", [32, 96, 160, 256])
+@pytest.mark.parametrize("m,e,top_k,n", [(8, 16, 8, 40), (160, 16, 4, 130)],
+                         ids=["blk16", "blk32"])
+def test_soft_op_fp32_stage_counts(k, m, e, top_k, n):
+    rng = np.random.default_rng(k * 3 + m)
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(k + m, (m, k)).float()
+    w, ids = _route_with_dropped(m, e, top_k, 6000 + k + m, 5)
+    C = _run(a, None, wp, ws, ids, w, torch.float32, True)
+    out = C.cpu().numpy()
+    assert not np.isnan(out).any(), "a row of C was left unwritten"
+    ids_np = ids.numpy()
+    assert np.all(out[(ids_np < 0) | (ids_np >= e)] == 0)
+    oracle = O.fused_moe_fp64(a.numpy(), wp, ws, 0.75, np.ones(e), w.numpy(), ids_np, True,
+                              compute_dtype="f32")
+    assert_parity(out, oracle, what=f"fp32 k={k} m={m} n={n}")
