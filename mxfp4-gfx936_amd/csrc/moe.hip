@@ -836,12 +836,23 @@ SoftPath soft_path(int a_dtype, int c_dtype, bool prepacked) {
   return prepacked ? SOFT_W4A16_PRE : SOFT_W4A16;
 }
 
-int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path) {
+// With a prepacked copy (AITER's entry on the copy, E=128, top-8, 32 vs
+// 64-row blocks, 16 / 24 / 32 / 48 routes per expert; us): 32 rows up to 16
+// routes per expert, 64 above 32, and between the two 64 where K >= 2048
+// (longer K streams more weight bytes per padded row): N=1536 K=2048 40.1 /
+// 43.9 / 50.7 / 50.8 vs 42.8 / 44.0 / 44.6 / 47.2; N=1024 K=4096 52.0 /
+// 67.4 / 65.7 / 78.2 vs 55.8 / 59.3 / 61.6 / 65.4; N=3072 K=2048 83.7 /
+// 106.7 / 108.7 / 113.0 vs 94.6 / 98.1 / 100.0 / 107.0; N=2048 K=3072 91.2
+// / 114.0 / 106.0 / 141.6 vs 105.9 / 108.7 / 113.0 / 119.2; N=2048 K=768
+// 23.1 / 27.3 / 27.5 / 35.7 vs 29.9 / 30.5 / 31.2 / 33.8; N=4096 K=1024
+// 75.0 / 73.4 / 73.4 / 91.7 vs 73.9 / 76.9 / 79.4 / 88.1.  The packed /
+// FP8 path keeps 32 up to 32 routes per expert, else 64.
+int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path, int64_t k) {
   const double avg = (double)routes / (double)(num_experts > 0 ? num_experts : 1);
   if (avg <= 1.5) return 16;
   if (path == SOFT_F32) return avg <= 8.0 ? 16 : 32;
-  // prepacked weights: the MoE layer's rule (tiles tuned on that layout)
-  if (path != SOFT_W4A16) return avg <= 32.0 ? 32 : 64;
+  if (path == SOFT_W4A16_PRE) return avg <= 16.0 ? 32 : (avg > 32.0 || k >= 2048 ? 64 : 32);
+  if (path == SOFT_SCALED) return avg <= 32.0 ? 32 : 64;
   return avg <= 28.0 ? 32 : (avg <= 56.0 ? 64 : 128);
 }
 
@@ -854,9 +865,9 @@ struct SoftPlan {
   int64_t off_counts, off_sorted, off_experts, off_npp, total;
 };
 
-SoftPlan plan_soft(int64_t routes, int64_t num_experts, SoftPath path) {
+SoftPlan plan_soft(int64_t routes, int64_t num_experts, SoftPath path, int64_t k) {
   SoftPlan p;
-  p.block_m = soft_block_m(routes, num_experts, path);
+  p.block_m = soft_block_m(routes, num_experts, path, k);
   p.zero_c = num_experts + 1 > kMaxExperts;
   p.align_experts = (int)(p.zero_c ? num_experts : num_experts + 1);
   p.drop_to = p.zero_c ? -1 : (int)num_experts;
@@ -943,10 +954,15 @@ extern "C" int mxfp4_fused_moe_workspace_size(int64_t m, int top_k, int64_t num_
               (long long)num_experts);
     return MXFP4_ERR_VALUE;
   }
-  // either layout's plan fits (the caller may pass a prepacked copy)
-  const int64_t x = plan_soft(m * top_k, num_experts, soft_path(a_dtype, c_dtype, false)).total;
-  const int64_t y = plan_soft(m * top_k, num_experts, soft_path(a_dtype, c_dtype, true)).total;
-  *bytes = x > y ? x : y;
+  // every plan fits: either layout (the caller may pass a prepacked copy),
+  // any K
+  int64_t most = 0;
+  for (int pre = 0; pre < 2; ++pre)
+    for (int64_t k : {(int64_t)0, (int64_t)1 << 30}) {
+      const int64_t t = plan_soft(m * top_k, num_experts, soft_path(a_dtype, c_dtype, pre), k).total;
+      most = t > most ? t : most;
+    }
+  *bytes = most;
   return MXFP4_OK;
 }
 
@@ -986,7 +1002,8 @@ extern "C" int mxfp4_fused_moe_pre(const void* a, int a_dtype, int64_t a_rows,
     return MXFP4_ERR_VALUE;
   }
   const int64_t routes = m * top_k;
-  const SoftPlan p = plan_soft(routes, num_experts, soft_path(a_dtype, c_dtype, pre_b != nullptr));
+  const SoftPlan p =
+      plan_soft(routes, num_experts, soft_path(a_dtype, c_dtype, pre_b != nullptr), k);
   int rc = check_routed_args(a, a_dtype, a_row_stride, a_mx, b, num_experts, n, k, c_dtype, top_k,
                              p.block_m, p.max_sorted);
   if (rc) return rc;
