@@ -54,7 +54,7 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
 }
 
-template <int WGM, int WGN, int FM, int FN, int STAGES, bool PRE = false>
+template <int WGM, int WGN, int FM, int FN, int STAGES, bool PRE = false, int BG = 1>
 struct PfShape {
   static constexpr int NW = WGM * WGN;  // waves
   static constexpr int NT = 64 * NW;    // threads
@@ -65,6 +65,13 @@ struct PfShape {
   static constexpr int B_STAGE = BN * 32;   // BN rows x 64 nibbles
   static constexpr int A_TOT = BM / 8;      // 1 KB wave-loads per stage (8 rows each)
   static constexpr int B_TOT = BN / 32;     // (32 rows each)
+  // Original layout in weight-line groups (BG > 1): a weight row's BG x 32
+  // bytes (BG stages) in one piece, in two alternating group slots
+  static constexpr int RBB = 32 * BG;              // bytes of a row per group
+  static constexpr int B_GRP = BN * RBB;           // bytes per group slot
+  static constexpr int B_GTOT = B_GRP / 1024;      // 1 KB wave-loads per group
+  static constexpr int B_GPER = (B_GTOT + NW - 1) / NW;
+  static constexpr int B_REGION = BG > 1 ? 2 * B_GRP : STAGES * B_STAGE;
   // Scales.  Original layout: the 4 E8M0 bytes of a weight row's 128 K,
   // staged every other stage (a slot per stage pair), 4-byte lanes.
   // Prepacked: the 16-bit scale operand halves of a row's two 32-blocks of
@@ -86,7 +93,7 @@ struct PfShape {
   // scale slots: one per stage (prepacked) or stage pair, enough for every
   // stage in flight
   static constexpr int S_SLOTS = PRE ? STAGES : (STAGES + 2) / 2;
-  static constexpr int PIPE = STAGES * (A_STAGE + B_STAGE) + S_SLOTS * S_SLOT;
+  static constexpr int PIPE = STAGES * A_STAGE + B_REGION + S_SLOTS * S_SLOT;
   // loads a wave issues for one stage (the prepacked scales come every stage;
   // the original ones every other, which waiting for this count covers)
   static constexpr int PER_STAGE = A_PER + B_PER + (PRE ? S_PER : 0);
@@ -113,10 +120,10 @@ constexpr int epi_passes(int bm, int row_bytes, int pipe_bytes) {
 // lane), and the high halves of its two scale operands one dword of the
 // group's 64-byte scale block (s_rd = group block + 4 * row): conflict-free
 // reads, one shift or mask per scale.
-template <typename T, int FM, int FN, bool PRE>
+template <typename T, int FM, int FN, bool PRE, int RB = 32>
 __device__ __forceinline__ void stage_math(const uint8_t* As, const uint8_t* Bs, const uint8_t* Ss,
                                            int a_rd0, int b_rd, int b_sw, int s_rd,
-                                           f32x4 (&acc)[FM][FN]) {
+                                           f32x4 (&acc)[FM][FN], int cb = 0) {
   typedef typename V8Of<T>::type V8;
   V8 af[2][FM];
   uint32_t raw[2][FN];
@@ -142,7 +149,7 @@ __device__ __forceinline__ void stage_math(const uint8_t* As, const uint8_t* Bs,
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         raw[ks][fn] =
-            *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 16 * 32 + ((ks ^ b_sw) * 16));
+            *reinterpret_cast<const uint32_t*>(Bs + b_rd + fn * 16 * RB + (((cb + ks) ^ b_sw) * 16));
         sc[ks][fn] = e8m0_scale(Ss[s_rd + fn * 16 * 4 + ks]);
       }
     }
@@ -159,9 +166,10 @@ __device__ __forceinline__ void stage_math(const uint8_t* As, const uint8_t* Bs,
   }
 }
 
-template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB, bool PRE>
+template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB, bool PRE,
+          int BG = 1>
 __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int nbm, int nbn) {
-  typedef PfShape<WGM, WGN, FM, FN, STAGES, PRE> S;
+  typedef PfShape<WGM, WGN, FM, FN, STAGES, PRE, BG> S;
   constexpr int BM = S::BM, BN = S::BN, NT = S::NT;
   constexpr int OUT_COLS = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int ES = (EPI == EPI_PARTIAL) ? 4 : 2;  // bytes per output element
@@ -174,10 +182,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   static_assert(STAGES >= 2 && STAGES <= 8, "2 to 8 stages");
   static_assert((STAGES - 2) * S::PER_STAGE <= 63, "vmcnt holds at most 63");
   static_assert(EPI != EPI_SILU_MUL || FN % 2 == 0, "SiLU pairs need even FN");
+  static_assert(BG == 1 || (!PRE && EPI != EPI_PARTIAL && STAGES <= 3 && BG <= 4 &&
+                            S::B_GTOT % S::NW == 0),
+                "weight-line groups: original layout, whole K, at most 3 stages");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
   uint8_t* const sA = smem;
   uint8_t* const sB = smem + STAGES * S::A_STAGE;
-  uint8_t* const sS = smem + STAGES * (S::A_STAGE + S::B_STAGE);
+  uint8_t* const sS = smem + STAGES * S::A_STAGE + S::B_REGION;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -257,11 +268,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   // Prepacked: B wave-load q holds groups 2q and 2q + 1 (lanes 0-31, 32-63;
   // 16 bytes each of the group's 512-byte stage block); scale byte b of the
   // stage's scale region is byte b % 64 of group b / 64's 64-byte block.
-  uint32_t b_off[S::B_PER];
+  // Weight-line groups: wave-load q holds rows q * 64 / CPRB .., lane l
+  // filling slot l % CPRB of its row with the chunk that belongs there
+  // (chunk c of row r sits in slot c ^ (r * BG / 8) % CPRB: the 16 rows of a
+  // fragment read hit all 64 banks).
+  constexpr int BPW = BG > 1 ? S::B_GPER : S::B_PER;
+  uint32_t b_off[BPW];
 #pragma unroll
-  for (int j = 0; j < S::B_PER; ++j) {
+  for (int j = 0; j < BPW; ++j) {
     const int q = j * S::NW + wave;
-    if constexpr (PRE) {
+    if constexpr (BG > 1) {
+      constexpr int CPRB = 2 * BG;
+      const int row = q * (64 / CPRB) + lane / CPRB;
+      const int c = (lane % CPRB) ^ ((row * BG / 8) % CPRB);
+      const int grow = q < S::B_GTOT ? weight_row(row) : -1;
+      b_off[j] = grow >= 0 ? (uint32_t)(grow * g.b_n) + c * 16 : kOOB;
+    } else if constexpr (PRE) {
       const int gt = 2 * q + (lane >> 5);
       const int grow = (q < S::B_TOT && gt < S::GRP) ? weight_row(gt * 16) : -1;
       b_off[j] = grow >= 0 ? (uint32_t)((grow >> 4) * nk_all * 512) + (lane & 31) * 16 : kOOB;
@@ -297,6 +319,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   }
   auto issue = [&](int kt) {
     const int st = kt % STAGES;
+    if constexpr (BG > 1) {
+      // stages kt .. kt + BG - 1 of every weight row, with the first of them
+      if (kt % BG == 0) {
+        uint8_t* const slot = sB + ((kt / BG) & 1) * S::B_GRP;
+#pragma unroll
+        for (int j = 0; j < BPW; ++j)
+          llvm_amdgcn_raw_buffer_load_lds(rB, lds_ptr(slot + (j * S::NW + wave) * 1024), 16,
+                                          (int)b_off[j], kt * 32, 0, 0);
+      }
+    }
     if constexpr (PRE) {
 #pragma unroll
       for (int j = 0; j < S::S_PER; ++j) {
@@ -321,20 +353,32 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
         llvm_amdgcn_raw_buffer_load_lds(rA, lds_ptr(sA + st * S::A_STAGE + q * 1024), 16,
                                         (int)a_off[j], kt * 128, 0, 0);
     }
+    if constexpr (BG == 1) {
 #pragma unroll
-    for (int j = 0; j < S::B_PER; ++j) {
-      const int q = j * S::NW + wave;
-      if (S::B_TOT % S::NW == 0 || q < S::B_TOT)
-        llvm_amdgcn_raw_buffer_load_lds(rB, lds_ptr(sB + st * S::B_STAGE + q * 1024), 16,
-                                        (int)b_off[j], kt * (PRE ? 512 : 32), 0, 0);
+      for (int j = 0; j < S::B_PER; ++j) {
+        const int q = j * S::NW + wave;
+        if (S::B_TOT % S::NW == 0 || q < S::B_TOT)
+          llvm_amdgcn_raw_buffer_load_lds(rB, lds_ptr(sB + st * S::B_STAGE + q * 1024), 16,
+                                          (int)b_off[j], kt * (PRE ? 512 : 32), 0, 0);
+      }
     }
+  };
+  // weight-line groups: this wave's loads of stage x (a per-wave count: the
+  // A and scale wave-loads need not divide among the waves)
+  int a_w = 0, s_w = 0;
+#pragma unroll
+  for (int j = 0; j < S::A_PER; ++j) a_w += (S::A_TOT % S::NW == 0 || j * S::NW + wave < S::A_TOT);
+#pragma unroll
+  for (int j = 0; j < S::S_PER; ++j) s_w += (j * S::NW + wave < S::S_TOT);
+  auto stage_loads = [&](int x) {
+    return a_w + (x % BG == 0 ? S::B_GPER : 0) + ((x & 1) == 0 ? s_w : 0);
   };
 
   // ---- per-lane LDS read offsets (fragment rows differ from c16 by
   // multiples of 16, so the swizzle terms are lane constants)
   const int a_rd0 = (wm * FM * 16 + c16) * 128 + ((grp ^ (c16 & 7)) * 16);
-  const int b_sw = (c16 >> 3) & 1;
-  const int b_rd = (wn * FN * 16 + c16) * 32 + grp * 4;
+  const int b_sw = (c16 * BG / 8) % (2 * BG);
+  const int b_rd = (wn * FN * 16 + c16) * S::RBB + grp * 4;
   const int s_rd = (wn * FN * 16 + c16) * 4;
   const int b_rd_pre = wn * FN * 512 + lane * 8;  // group wn*FN's block, lane's 8 bytes
   const int s_rd_pre = wn * FN * 64 + c16 * 4;    // group wn*FN's scales, row c16
@@ -361,14 +405,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     // original layout, one scale load on even stages, which waiting for
     // PER_STAGE covers)
     const int later = (k_end - 1 - kt) < (STAGES - 2) ? (k_end - 1 - kt) : (STAGES - 2);
-    static_for<0, STAGES - 1>([&](auto c) {
-      if (later == decltype(c)::value) wait_vmcnt<decltype(c)::value * S::PER_STAGE>();
-    });
+    if constexpr (BG > 1) {
+      // at most one later stage in flight (STAGES <= 3): its exact count
+      const int cnt = later > 0 ? stage_loads(kt + 1) : 0;
+      static_for<0, S::A_PER + S::B_GPER + S::S_PER + 1>([&](auto c) {
+        if (cnt == decltype(c)::value) wait_vmcnt<decltype(c)::value>();
+      });
+    } else {
+      static_for<0, STAGES - 1>([&](auto c) {
+        if (later == decltype(c)::value) wait_vmcnt<decltype(c)::value * S::PER_STAGE>();
+      });
+    }
     barrier_only();
     if (kt + STAGES - 1 < k_end) issue(kt + STAGES - 1);
     if constexpr (PRE)
       stage_math<T, FM, FN, true>(sA + (kt % STAGES) * S::A_STAGE, sB + (kt % STAGES) * S::B_STAGE,
                                   sS + (kt % STAGES) * S::S_SLOT, a_rd0, b_rd_pre, 0, s_rd_pre, acc);
+    else if constexpr (BG > 1)
+      stage_math<T, FM, FN, false, S::RBB>(
+          sA + (kt % STAGES) * S::A_STAGE, sB + ((kt / BG) & 1) * S::B_GRP,
+          sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2, a_rd0, b_rd, b_sw, s_rd, acc,
+          2 * (kt % BG));
     else
       stage_math<T, FM, FN, false>(sA + (kt % STAGES) * S::A_STAGE, sB + (kt % STAGES) * S::B_STAGE,
                                    sS + ((kt >> 1) % S::S_SLOTS) * S::S_SLOT + (kt & 1) * 2, a_rd0,
@@ -842,9 +899,15 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
   }
 }
 
-template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB, bool PRE>
+template <typename T, int WGM, int WGN, int FM, int FN, int STAGES, int EPI, int MINB, bool PRE,
+          int BG = 1>
 int launch_cfg(const GemmArgs& g, hipStream_t st) {
   typedef PfShape<WGM, WGN, FM, FN, STAGES, PRE> S;
+  // weight-line groups where the configuration takes them (else per stage)
+  constexpr int BGV = (BG > 1 && !PRE && EPI != EPI_PARTIAL && STAGES <= 3 && STAGES - 1 <= BG &&
+                       (S::BN * 32 * BG / 1024) % S::NW == 0)
+                          ? BG
+                          : 1;
   const int out_cols = (EPI == EPI_SILU_MUL) ? S::BN / 2 : S::BN;
   const int nbn = (g.n + out_cols - 1) / out_cols;
   int64_t nbm = (g.m + S::BM - 1) / S::BM;
@@ -855,7 +918,8 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
     set_error("w4a16 prefill: bad grid");
     return MXFP4_ERR_VALUE;
   }
-  if constexpr (EPI != EPI_PARTIAL && WGM == 1 && WGN == 4 && STAGES == 2 && FN <= 4) {
+  if constexpr (BGV == 1 && EPI != EPI_PARTIAL && WGM == 1 && WGN == 4 && STAGES == 2 &&
+                FN <= 4) {
     // routed grid of more tiles than resident workgroups: the persistent
     // kernel (dense grids run 2-5% slower in it: their tiles start with
     // one load round trip, not the routed two, and gain nothing)
@@ -879,7 +943,7 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
       }
     }
   }
-  w4a16_pf<T, WGM, WGN, FM, FN, STAGES, EPI, MINB, PRE><<<(unsigned)nwg, S::NT, 0, st>>>(
+  w4a16_pf<T, WGM, WGN, FM, FN, STAGES, EPI, MINB, PRE, BGV><<<(unsigned)nwg, S::NT, 0, st>>>(
       g, (int)nbm, nbn);
   return launch_status("w4a16 prefill launch");
 }
@@ -942,9 +1006,50 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
   }
 }
 
+// Checkpoint-layout weights in weight-line groups (a row's 32 bytes of BG
+// stages in one piece: 1/BG of the L1 -> L2 requests for the weights, at
+// 2 x BG x 32 bytes of LDS per weight row) where that measured faster, the
+// same configurations as launch_pf_typed otherwise (bitwise the same
+// results).  Measured (one job, eager loops, us, per-stage -> groups):
+// 32 x 128 with 2-stage groups -- soft op (E=128, top-8, K=2048, N=1536)
+// 64 / 128 / 256 / 384 tokens 53.4 / 54.7 / 56.7 / 63.0 -> 52.9 / 53.5 /
+// 55.4 / 55.4, MoE layer 128 / 256 tokens 101.5 / 108.9 -> 94.5 / 99.5,
+// AITER's entry with BLOCK_SIZE_M 32 at 512 tokens 66.1 -> 55.9 (4-stage
+// groups: better at 64-256 tokens, 60.6 at 384); dense 64 x 128 with
+// 2-stage groups -- qkv K=2048 N=5120 M=1024 30.6 -> 28.7 (routed 64 x 128
+// lost: soft op 512 tokens 64.2 -> 66.9); dense 128 x 128 with 2-stage
+// groups -- o_proj K=4096 N=2048 M=4096 63.8 -> 61.4, qkv M=2048 44.2 ->
+// 43.5 (4-stage groups: 60.7 and 48.6); the one-round dense
+// 256-row tiles with 4-stage groups -- qkv M=4096 / 8192 70.9 / 140.6 ->
+// 69.8 / 138.0 (128 x 320 with 4-stage groups lost: one workgroup per CU,
+// qkv M=8192 173.9).
+template <typename T, int EPI>
+int launch_pf_checkpoint(const GemmArgs& g, int cfg, hipStream_t st) {
+  if constexpr (EPI != EPI_PARTIAL) {
+    const bool dense = g.sorted_ids == nullptr;
+    switch (cfg) {
+      case PF_32x128: return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4, false, 2>(g, st);
+      case PF_64x128:
+        if (dense) return launch_cfg<T, 1, 4, 4, 2, 3, EPI, 3, false, 2>(g, st);
+        break;
+      case PF_128x128:
+        if (dense) return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2, false, 2>(g, st);
+        break;
+      case PF_256x320:
+        if constexpr (EPI == EPI_STORE) return launch_cfg<T, 2, 4, 8, 5, 2, EPI, 1, false, 4>(g, st);
+        break;
+      case PF_256x256:
+        if constexpr (EPI == EPI_STORE) return launch_cfg<T, 2, 4, 8, 4, 2, EPI, 1, false, 4>(g, st);
+        break;
+      default: break;
+    }
+  }
+  return launch_pf_typed<T, EPI, false>(g, cfg, st);
+}
+
 template <typename T, int EPI>
 int launch_pf_layout(const GemmArgs& g, int cfg, hipStream_t st) {
-  if (!pf_prepacked_usable(g)) return launch_pf_typed<T, EPI, false>(g, cfg, st);
+  if (!pf_prepacked_usable(g)) return launch_pf_checkpoint<T, EPI>(g, cfg, st);
   GemmArgs p = g;
   p.b = g.pre_b;
   p.bs = reinterpret_cast<const uint8_t*>(g.pre_s);
