@@ -853,7 +853,11 @@ int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path, int64_t k) 
   if (path == SOFT_F32) return avg <= 8.0 ? 16 : 32;
   if (path == SOFT_W4A16_PRE) return avg <= 16.0 ? 32 : (avg > 32.0 || k >= 2048 ? 64 : 32);
   if (path == SOFT_SCALED) return avg <= 32.0 ? 32 : 64;
-  return avg <= 28.0 ? 32 : (avg <= 56.0 ? 64 : 128);
+  // checkpoint layout above 56 routes per expert: 128 rows only for long K
+  // (AITER's entry, 64 / 128 / 256 routes per expert, 64 vs 128 rows: K=768
+  // N=2048 46.8 / 75.5 / 130.9 vs 50.6 / 79.0 / 132.5 us; K=2048 N=1536
+  // 84.1 / 129.7 / 235.6 vs 80.8 / 129.0 / 229.5)
+  return avg <= 28.0 ? 32 : (avg <= 56.0 || k < 2048 ? 64 : 128);
 }
 
 struct SoftPlan {
