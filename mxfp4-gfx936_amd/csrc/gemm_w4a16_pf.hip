@@ -1015,23 +1015,34 @@ int launch_pf_typed(const GemmArgs& g, int cfg, hipStream_t st) {
 // 64 / 128 / 256 / 384 tokens 53.4 / 54.7 / 56.7 / 63.0 -> 52.9 / 53.5 /
 // 55.4 / 55.4, MoE layer 128 / 256 tokens 101.5 / 108.9 -> 94.5 / 99.5,
 // AITER's entry with BLOCK_SIZE_M 32 at 512 tokens 66.1 -> 55.9 (4-stage
-// groups: better at 64-256 tokens, 60.6 at 384); dense 64 x 128 with
+// groups: better at 64-256 tokens, 60.6 at 384; dense 32 x 128 lost: qkv
+// K=2048 N=5120 M=370 15.7 -> 16.9); dense 64 x 128 with
 // 2-stage groups -- qkv K=2048 N=5120 M=1024 30.6 -> 28.7 (routed 64 x 128
 // lost: soft op 512 tokens 64.2 -> 66.9); dense 128 x 128 with 2-stage
 // groups -- o_proj K=4096 N=2048 M=4096 63.8 -> 61.4, qkv M=2048 44.2 ->
 // 43.5 (4-stage groups: 60.7 and 48.6); the one-round dense
 // 256-row tiles with 4-stage groups -- qkv M=4096 / 8192 70.9 / 140.6 ->
 // 69.8 / 138.0 (128 x 320 with 4-stage groups lost: one workgroup per CU,
-// qkv M=8192 173.9).
+// qkv M=8192 173.9).  Routed 32 x 256 with 2-stage groups: AITER's entry
+// (BLOCK_SIZE_M 32, K=2048 N=1536) at 768 / 1024 tokens 79.9 / 97.0 ->
+// 67.4 / 83.7; routed 64 x 128 as a 2-stage pipeline with 2-stage groups
+// (four workgroups per CU; the 3-stage one with groups holds three and
+// lost): 1024 tokens 87.3 -> 80.1, 512 / 768 tokens within 0.5.
 template <typename T, int EPI>
 int launch_pf_checkpoint(const GemmArgs& g, int cfg, hipStream_t st) {
   if constexpr (EPI != EPI_PARTIAL) {
     const bool dense = g.sorted_ids == nullptr;
     switch (cfg) {
-      case PF_32x128: return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4, false, 2>(g, st);
+      case PF_32x128:
+        if (!dense) return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4, false, 2>(g, st);
+        break;
+      case PF_32x256:
+        if (!dense) return launch_cfg<T, 1, 4, 2, 4, 3, EPI, 3, false, 2>(g, st);
+        break;
       case PF_64x128:
         if (dense) return launch_cfg<T, 1, 4, 4, 2, 3, EPI, 3, false, 2>(g, st);
-        break;
+        // routed: two stages in flight keep four workgroups per CU
+        return launch_cfg<T, 1, 4, 4, 2, 2, EPI, 4, false, 2>(g, st);
       case PF_128x128:
         if (dense) return launch_cfg<T, 1, 4, 8, 2, 2, EPI, 2, false, 2>(g, st);
         break;
