@@ -201,6 +201,7 @@ enum P4Config {
   P4_256x256 = 0,  // 2 x 4 waves of 128 x 64, 3 stages
   P4_128x128 = 1,  // 1 x 4 waves of 128 x 32
   P4_64x128 = 2,   // 1 x 4 waves of 64 x 32
+  P4_32x128 = 3,   // 1 x 4 waves of 32 x 32 (routed 32-row blocks)
 };
 bool p4_supported(const GemmArgs& g);
 int p4_choose(const GemmArgs& g, int out_dtype);  // -1: not applicable

@@ -392,6 +392,7 @@ int launch_typed(const GemmArgs& g, int cfg, hipStream_t st) {
     switch (cfg) {
       case P4_256x256: return launch_cfg<TO, AF, 2, 4, 8, 4, 1, 3, 3, 1>(g, st);
       case P4_128x128: return launch_cfg<TO, AF, 1, 4, 8, 2, 2, 3, 3, 1>(g, st);
+      case P4_32x128: return launch_cfg<TO, AF, 1, 4, 2, 2, 4, 2, 2, 1>(g, st);
       default: return launch_cfg<TO, AF, 1, 4, 4, 2, 2, 2, 2, 1>(g, st);  // P4_64x128
     }
   } else {
@@ -404,6 +405,7 @@ int launch_typed(const GemmArgs& g, int cfg, hipStream_t st) {
     switch (cfg) {
       case P4_256x256: return launch_cfg<TO, 4, 2, 4, 8, 4, 1, 3, 2, 2>(g, st);
       case P4_128x128: return launch_cfg<TO, 4, 1, 4, 8, 2, 2, 2, 2, 2>(g, st);
+      case P4_32x128: return launch_cfg<TO, 4, 1, 4, 2, 2, 4, 2, 2, 1>(g, st);
       default: return launch_cfg<TO, 4, 1, 4, 4, 2, 2, 2, 2, 1>(g, st);  // P4_64x128
     }
   }
@@ -433,6 +435,8 @@ int p4_choose(const GemmArgs& g, int out_dtype) {
   if (allowed(256) && tiles(256, 256) >= 256) return P4_256x256;
   if (allowed(128) && tiles(128, 128) >= 128) return P4_128x128;
   if (allowed(64)) return P4_64x128;
+  // routed 32-row blocks (the register-staged kernel took them before)
+  if (allowed(32)) return P4_32x128;
   return -1;
 }
 
