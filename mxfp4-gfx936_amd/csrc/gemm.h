@@ -52,6 +52,10 @@ struct GemmArgs {
   // its expert, together with the next 15 routes of that expert.
   const void* route_ids;
   int32_t ids64;
+  // direct routing: a route whose id is outside [0, num_experts) writes
+  // zeros to its output row (the soft op, every row of C written) instead
+  // of being skipped (the MoE layer, whose combine skips it)
+  int32_t zero_dropped;
   // Split K (dense, plain epilogue): `splitk` K slices, slice s written as
   // FP32 to splitk_ws + s * m * n, then summed by splitk_reduce.
   float* splitk_ws;

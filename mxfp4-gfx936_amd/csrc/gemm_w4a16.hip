@@ -115,7 +115,13 @@ __device__ __forceinline__ int direct_rows(const GemmArgs& g, int r, int c16, in
       e = (int64_t)(((uint64_t)ehi << 32) | elo);
     }
   }
-  if (e < 0 || e >= g.num_experts) return 1;
+  if (e < 0 || e >= g.num_experts) {
+    if (!g.zero_dropped) return 1;
+    // the route's row alone, through the expert -1 path (zeros)
+    *expert = -1;
+    my_route[0] = c16 == 0 ? r : -1;
+    return 0;
+  }
   int rank = 0, got = 0;
   my_route[0] = -1;
 #pragma unroll

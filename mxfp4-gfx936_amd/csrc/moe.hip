@@ -1022,6 +1022,21 @@ extern "C" int mxfp4_fused_moe_pre(const void* a, int a_dtype, int64_t a_rows,
   }
   if (routes == 0) return MXFP4_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // Few routes on the W4A16 path: the decode kernels find each route's rows
+  // from the top-k ids (direct routing, as in the MoE layer), so no routing
+  // launch; a route whose id is outside [0, E) writes zeros to its row.
+  const SoftPath path = soft_path(a_dtype, c_dtype, pre_b != nullptr);
+  const int64_t lim = (int64_t)1 << 31;
+  if ((path == SOFT_W4A16 || path == SOFT_W4A16_PRE) && routes <= kDirectRoutes &&
+      n * (k / 2) < lim && a_rows * a_row_stride * elem_size(a_dtype) < lim) {
+    GemmArgs g = routed_args(a, a_rows, a_row_stride, a_mx, b, b_mx, num_experts, n, k, c, n,
+                             a_scale, b_scale, topk_weights, mul_routed_weight, nullptr, nullptr,
+                             nullptr, routes, 16, routes, top_k);
+    g.route_ids = topk_ids;
+    g.ids64 = ids_dtype == MXFP4_DT_I64;
+    g.zero_dropped = 1;
+    return dispatch_gemm(g, a_dtype, c_dtype, EPI_STORE, st);
+  }
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   int32_t* counts = reinterpret_cast<int32_t*>(ws + p.off_counts);
   int32_t* sorted = reinterpret_cast<int32_t*>(ws + p.off_sorted);

@@ -264,3 +264,26 @@ def test_soft_op_fp32_stage_counts(k, m, e, top_k, n):
     oracle = O.fused_moe_fp64(a.numpy(), wp, ws, 0.75, np.ones(e), w.numpy(), ids_np, True,
                               compute_dtype="f32")
     assert_parity(out, oracle, what=f"fp32 k={k} m={m} n={n}")
+
+
+@pytest.mark.parametrize("ids_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("m,top_k", [(1, 8), (3, 4), (8, 8)])
+def test_soft_op_direct_routing_writes_dropped_rows(m, top_k, ids_dtype):
+    # <= 64 routes on the W4A16 path: the decode kernels route from the ids
+    # themselves (no routing launch); a route with an id outside [0, E) gets
+    # a row of zeros from its own workgroup
+    e, k, n = 32, 512, 96
+    rng = np.random.default_rng(m * 10 + top_k)
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(m + 90, (m, k))
+    w, ids = _route_with_dropped(m, e, top_k, 7000 + m, max(1, m * top_k // 4))
+    ids = ids.to(ids_dtype)
+    C = _run(a, None, wp, ws, ids, w, torch.bfloat16, True)
+    out = C.float().cpu().numpy()
+    assert not np.isnan(out).any(), "a row of C was left unwritten"
+    ids_np = ids.numpy().astype(np.int64)
+    bad = (ids_np < 0) | (ids_np >= e)
+    assert bad.any() and np.all(out[bad] == 0)
+    oracle = O.fused_moe_fp64(O.round_to_dtype(a.float().numpy(), "bf16"), wp, ws, 0.75,
+                              np.ones(e), w.numpy(), ids_np, True, compute_dtype="bf16")
+    assert_parity(out, oracle, what=f"direct m={m} top_k={top_k} {ids_dtype}")
