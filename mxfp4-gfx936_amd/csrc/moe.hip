@@ -853,6 +853,13 @@ int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path, int64_t k) 
   if (path == SOFT_F32) return avg <= 8.0 ? 16 : 32;
   if (path == SOFT_W4A16_PRE) return avg <= 16.0 ? 32 : (avg > 32.0 || k >= 2048 ? 64 : 32);
   if (path == SOFT_SCALED) return avg <= 32.0 ? 32 : 64;
+  // checkpoint layout, long K: 16-row blocks (the single-trip decode
+  // kernels) up to 4 routes per expert (AITER's entry, graph replays,
+  // K=2048 N=1536, 3 / 4 / 6 / 8 / 12 / 16 routes per expert, 16 vs 32
+  // rows: 42.0 / 47.8 / 52.3 / 55.7 / 60.1 / 63.2 vs 45.2 / 56.6 / 58.1 /
+  // 58.6 / 59.4 / 59.6 us; K=768 N=2048 takes 32 rows from 1.5 routes per
+  // expert: 27.8 / 31.9 / 34.5 vs 24.1 / 27.3 / 29.4 at 3 / 4 / 6)
+  if (k >= 2048 && avg <= 4.0) return 16;
   // checkpoint layout above 56 routes per expert: 128 rows only for long K
   // (AITER's entry, 64 / 128 / 256 routes per expert, 64 vs 128 rows: K=768
   // N=2048 46.8 / 75.5 / 130.9 vs 50.6 / 79.0 / 132.5 us; K=2048 N=1536
