@@ -691,7 +691,12 @@ LayerPlan plan_layer(int64_t m, int top_k, int num_experts, int64_t hidden, int6
   // 128 x 256 on 128-row ones (pf_choose).  Layer, graph replays (E=128,
   // top-8, H=2048, I=768): 256 tokens 112.0 -> 108.8 us, 512 153.2 ->
   // 126.1, 1024 185.5 -> 160.2, 2048 246.7 -> 242.5, 4096 418.2 -> 414.4.
-  if (!prepacked) p.block_m = avg <= 1.5 ? 16 : (avg <= 28.0 ? 32 : (avg <= 56.0 ? 64 : 128));
+  // With the weight-line groups of the checkpoint tiles, 16-row blocks (the
+  // single-trip decode kernels) win up to 6 routes per expert (layer, graph
+  // replays over 3 weight copies, 32 / 48 / 64 / 96 tokens: 82.2 / 85.4 /
+  // 88.4 / 94.8 vs 92.1 / 93.4 / 97.2 / 98.5 us with 32 rows; the
+  // prepacked layer keeps 32 rows: 75.0-78.1 vs 82.2-94.8 us).
+  if (!prepacked) p.block_m = avg <= 6.0 ? 16 : (avg <= 28.0 ? 32 : (avg <= 56.0 ? 64 : 128));
   align_capacity(p.routes, num_experts, p.block_m, &p.max_sorted, &p.max_blocks, &p.nchunks);
   int64_t off = 0;
   p.off_counts = off; off = round_up(off + (p.nchunks > 0 ? p.nchunks : 1) * num_experts * 4, 256);
