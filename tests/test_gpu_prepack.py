@@ -35,8 +35,10 @@ def test_prepack_bytes_match_layout(e, rows, k):
 # (m, k, n): 128 x 320 tiles (the qkv headline), 128 x 256, 64 x 128,
 # split K (o_proj at 370 tokens), 32 x 128, a ragged N (partial 16-row
 # group), the skinny decode kernel (no prefill kernel: copy unused)
+# (1536, 2048, 5120): dense 128 x 128 tiles, which read checkpoint weights in
+# 2-stage weight-line groups
 LINEAR_CASES = [(4096, 2048, 5120), (4096, 4096, 4096), (1024, 2048, 5120), (370, 4096, 2048),
-                (256, 2048, 1536), (300, 512, 200), (8, 2048, 5120)]
+                (256, 2048, 1536), (300, 512, 200), (8, 2048, 5120), (1536, 2048, 5120)]
 
 
 @pytest.mark.parametrize("m,k,n", LINEAR_CASES)
@@ -165,3 +167,42 @@ def test_registered_dense_copy_serves_the_reference_signature():
         assert torch.equal(mx.linear_mxfp4_soft(x, w, s), after)
     finally:
         P.unregister_prepacked(w)
+
+
+def test_routed_32x256_line_groups_bitwise():
+    # AITER's entry with BLOCK_SIZE_M 32 at 1024 tokens, E=128, top-8: more
+    # than ten 32 x 128 tiles per CU, so the checkpoint layout runs 32 x 256
+    # tiles with 2-stage weight-line groups; the registered prepacked copy
+    # runs its own 32-row tiles; bitwise the same C, and sampled rows on the
+    # FP64 oracle
+    from mxfp4_amd import prepack as P
+    from oracle import mxfp4_oracle as O
+    from _helpers import assert_parity
+    rng = np.random.default_rng(1024)
+    m, e, top_k, k, n = 1024, 128, 8, 2048, 1536
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    B, Bs = cuda(wp), cuda(ws)
+    a = cuda(rand_act(1025, (m, k)))
+    g = torch.Generator().manual_seed(1026)
+    tw, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
+    tw, ids = tw.cuda(), ids.cuda()
+    srt, eid, npp = mx.make_routing_device(ids, e, 32)
+    one, ones_e = torch.ones(1, device="cuda"), torch.ones(e, device="cuda")
+
+    def run():
+        C = torch.full((m, top_k, n), 3.0, dtype=torch.bfloat16, device="cuda")
+        mx.fused_moe_mxfp4(a, B, C, one, ones_e, None, Bs, tw, ids, srt, eid, npp, True, top_k,
+                           False, False, {"BLOCK_SIZE_M": 32}, torch.bfloat16)
+        return C
+    plain = run()
+    P.register_prepacked(B, Bs)
+    try:
+        fast = run()
+    finally:
+        P.unregister_prepacked(B)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, fast)
+    rows = np.arange(0, m, 53)
+    oracle = O.fused_moe_fp64(a.float().cpu().numpy()[rows], wp, ws, 1.0, np.ones(e),
+                              tw.cpu().numpy()[rows], ids.cpu().numpy()[rows], True)
+    assert_parity(plain.float().cpu().numpy()[rows], oracle, what="routed 32 x 256 groups")
