@@ -869,7 +869,11 @@ int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path, int64_t k) 
   // (AITER's entry, 64 / 128 / 256 routes per expert, 64 vs 128 rows: K=768
   // N=2048 46.8 / 75.5 / 130.9 vs 50.6 / 79.0 / 132.5 us; K=2048 N=1536
   // 84.1 / 129.7 / 235.6 vs 80.8 / 129.0 / 229.5)
-  return avg <= 28.0 ? 32 : (avg <= 56.0 || k < 2048 ? 64 : 128);
+  // (32 rows up to 32 routes per expert: with the weight-line groups, on
+  // cold weights -- graph replays over 3 copies -- 32 vs 64 rows at 24 / 32
+  // / 40 routes per expert: K=2048 64.0 / 72.7 / 78.6 vs 72.6 / 76.1 / 73.3
+  // us, K=768 36.9 / 39.9 / 47.4 vs 40.1 / 40.7 / 42.3)
+  return avg <= 32.0 ? 32 : (avg <= 56.0 || k < 2048 ? 64 : 128);
 }
 
 struct SoftPlan {
