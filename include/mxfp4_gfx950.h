@@ -302,8 +302,7 @@ int mxfp4_moe_layer_pre(const void* x, int x_dtype, int64_t m, int64_t hidden, c
  * MXFP4_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs
  * on until the process ends; nothing is allocated per call.  Returns
  * MXFP4_ERR_VALUE when mxfp4_moe_layer_workspace_size exceeds that size
- * (at the BASELINE shape, E=128 top-8 hidden 2048 inter 768, up to ~700
- * tokens).  Calls that overlap on one GPU share the array and race: issue
+ * (with E=128, top-8, hidden 2048 and inter 768: up to ~700 tokens).  Calls that overlap on one GPU share the array and race: issue
  * them on one stream, or order them.  Otherwise as mxfp4_moe_layer.
  */
 #define MXFP4_NOALLOC_SCRATCH_BYTES (32LL << 20)
