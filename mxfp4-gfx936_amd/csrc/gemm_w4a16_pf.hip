@@ -458,6 +458,68 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
       }
     }
   }
+  if constexpr (EPI == EPI_STORE && FN >= 2) {
+    if (g.ldc % 8 == 0) {
+      // Straight from the registers (no LDS staging, no barrier): lane
+      // pairs (grp 0, 1) and (2, 3) trade halves with v_permlane16_swap so
+      // that each lane holds 8 consecutive columns of one block (even grp:
+      // block 2fp, odd grp: block 2fp + 1) and stores 16 bytes; an odd
+      // last block goes out as 8 bytes per lane.  Same arithmetic as the
+      // staged path below.
+      T* const cbase = static_cast<T*>(g.c);
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int trow = wm * FM * 16 + fm * 16 + c16;
+        const RowInfo r = row_info(g, pos0 + trow);
+        float rw = 1.0f;
+        if (g.route_w) rw = r.valid ? g.route_w[r.out_row] : 0.f;
+        T* const crow = cbase + (r.valid ? r.out_row : 0) * g.ldc;
+        auto outv = [&](int fn, int i) {
+          float o = acc[fm][fn][i] * alpha * rw;
+          if (g.bias) o += bv[fn][i];
+          return o;
+        };
+#pragma unroll
+        for (int fp = 0; fp < FN / 2; ++fp) {
+          uint32_t pv[2], qv[2];  // pv: block 2fp, qv: block 2fp + 1 (4 columns each)
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            pv[w] = pack2<T>(outv(2 * fp, 2 * w), outv(2 * fp, 2 * w + 1));
+            qv[w] = pack2<T>(outv(2 * fp + 1, 2 * w), outv(2 * fp + 1, 2 * w + 1));
+            const auto sw = __builtin_amdgcn_permlane16_swap(pv[w], qv[w], false, false);
+            pv[w] = sw[0];
+            qv[w] = sw[1];
+          }
+          const int col = ncol0 + wn * FN * 16 + (2 * fp + (grp & 1)) * 16 + (grp & 2) * 4;
+          if (!r.valid || col >= g.n) continue;
+          const uint32_t v[4] = {pv[0], pv[1], qv[0], qv[1]};
+          if (col + 8 <= g.n) {
+            *reinterpret_cast<i32x4*>(crow + col) =
+                i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+          } else {
+            for (int i = 0; i < 8 && col + i < g.n; ++i)
+              crow[col + i] = __builtin_bit_cast(T, (uint16_t)(v[i / 2] >> (16 * (i & 1))));
+          }
+        }
+        if constexpr (FN % 2 == 1) {
+          constexpr int fn = FN - 1;
+          const int col = ncol0 + wn * FN * 16 + fn * 16 + grp * 4;
+          const uint32_t v0 = pack2<T>(outv(fn, 0), outv(fn, 1));
+          const uint32_t v1 = pack2<T>(outv(fn, 2), outv(fn, 3));
+          if (r.valid && col < g.n) {
+            if (col + 4 <= g.n) {
+              *reinterpret_cast<uint2*>(crow + col) = uint2{v0, v1};
+            } else {
+              const uint32_t v[2] = {v0, v1};
+              for (int i = 0; i < 4 && col + i < g.n; ++i)
+                crow[col + i] = __builtin_bit_cast(T, (uint16_t)(v[i / 2] >> (16 * (i & 1))));
+            }
+          }
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int pass = 0; pass < EPI_PASSES; ++pass) {
     {
