@@ -621,12 +621,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
 // and epilogue arithmetic as w4a16_pf: results are bitwise equal.
 // Requirements (host): the w4a16_pf ones, 2 stages, 1 x 4 waves, output
 // columns and row stride multiples of 4, 8-byte aligned output and output
-// rows below 2 GiB.
+// rows below 2 GiB.  The epilogue stores 16 bytes per lane where columns
+// and row stride are multiples of 8 and the output 16-byte aligned, else 8.
 
 extern "C" __device__ void llvm_amdgcn_raw_buffer_store_v2i32(i32x2 vdata, i32x4 rsrc,
                                                               uint32_t voffset, int soffset,
                                                               int aux)
     __asm("llvm.amdgcn.raw.buffer.store.v2i32");
+extern "C" __device__ void llvm_amdgcn_raw_buffer_store_v4i32(i32x4 vdata, i32x4 rsrc,
+                                                              uint32_t voffset, int soffset,
+                                                              int aux)
+    __asm("llvm.amdgcn.raw.buffer.store.v4i32");
 
 template <typename T, int FM, int FN, int EPI, int MINB, bool PRE>
 __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int nbn,
@@ -796,6 +801,10 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
   const int b_rd_pre = wave * FN * 512 + lane * 8;
   const int s_rd_pre = wave * FN * 64 + c16 * 4;
   const i32x4 rC = make_rsrc(g.c, c_bytes);
+  // 16-byte stores where every 8-column run starting below N ends within
+  // it and the rows are 16-byte aligned
+  const bool wide =
+      g.n % 8 == 0 && g.ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(g.c) & 15) == 0;
 
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -911,41 +920,61 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
         for (int i = 0; i < 4; ++i)
           bv[fn][i] = g.bias ? t_bias(slot)[wave * FN * 16 + fn * 16 + grp * 4 + i] : 0.f;
     }
+    // output fragments of 16 columns: FN for a plain store, FN / 2 for
+    // SiLU*mul (gate fn, up fn + 1); outp packs values i, i + 1 of one
+    constexpr int OF = (EPI == EPI_SILU_MUL) ? FN / 2 : FN;
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-      if (EPI == EPI_SILU_MUL) {
+      auto outp = [&](int j, int i) -> uint32_t {
+        float o[2];
 #pragma unroll
-        for (int fn = 0; fn < FN; fn += 2) {
-          const int col = ncol0 + ((wave * FN + fn) >> 1) * 16 + grp * 4;
-          float h[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
+        for (int h = 0; h < 2; ++h) {
+          if constexpr (EPI == EPI_SILU_MUL) {
             // vllm:249-252 on tensors of T (as in w4a16_pf)
-            const T gb = from_f32<T>(acc[fm][fn][i] * alpha);
-            const T ub = from_f32<T>(acc[fm][fn + 1][i] * alpha);
+            const T gb = from_f32<T>(acc[fm][2 * j][i + h] * alpha);
+            const T ub = from_f32<T>(acc[fm][2 * j + 1][i + h] * alpha);
             const T sb = silu_round<T>(gb);
-            h[i] = expert >= 0 ? to_f32(sb) * to_f32(ub) : 0.f;
+            o[h] = expert >= 0 ? to_f32(sb) * to_f32(ub) : 0.f;
+          } else {
+            o[h] = acc[fm][j][i + h] * alpha * rw[fm];
+            if (g.bias) o[h] += bv[j < (EPI == EPI_STORE ? FN : 1) ? j : 0][i + h];
+            if (expert < 0) o[h] = 0.f;
           }
-          const uint32_t off =
-              (base[fm] != kOOB && col < g.n) ? base[fm] + col * (int)sizeof(T) : kOOB;
-          llvm_amdgcn_raw_buffer_store_v2i32(
-              i32x2{(int)pack2<T>(h[0], h[1]), (int)pack2<T>(h[2], h[3])}, rC, off, 0, 0);
+        }
+        return pack2<T>(o[0], o[1]);
+      };
+      auto offset = [&](int col) -> uint32_t {
+        return (base[fm] != kOOB && col < g.n) ? base[fm] + col * (int)sizeof(T) : kOOB;
+      };
+      if (OF >= 2 && wide) {
+        // lanes 16 apart trade fragment halves: each lane then holds 8
+        // consecutive columns of fragment 2fp (even grp) or 2fp + 1 (odd)
+#pragma unroll
+        for (int fp = 0; fp < OF / 2; ++fp) {
+          uint32_t pv[2], qv[2];
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            pv[w] = outp(2 * fp, 2 * w);
+            qv[w] = outp(2 * fp + 1, 2 * w);
+            const auto sw = __builtin_amdgcn_permlane16_swap(pv[w], qv[w], false, false);
+            pv[w] = sw[0];
+            qv[w] = sw[1];
+          }
+          const int col = ncol0 + wave * OF * 16 + (2 * fp + (grp & 1)) * 16 + (grp & 2) * 4;
+          llvm_amdgcn_raw_buffer_store_v4i32(
+              i32x4{(int)pv[0], (int)pv[1], (int)qv[0], (int)qv[1]}, rC, offset(col), 0, 0);
+        }
+        if constexpr (OF % 2 == 1) {
+          const int col = ncol0 + wave * OF * 16 + (OF - 1) * 16 + grp * 4;
+          llvm_amdgcn_raw_buffer_store_v2i32(i32x2{(int)outp(OF - 1, 0), (int)outp(OF - 1, 2)},
+                                             rC, offset(col), 0, 0);
         }
       } else {
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-          const int col = ncol0 + wave * FN * 16 + fn * 16 + grp * 4;
-          float o[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            o[i] = acc[fm][fn][i] * alpha * rw[fm];
-            if (g.bias) o[i] += bv[fn < (EPI == EPI_STORE ? FN : 1) ? fn : 0][i];
-            if (expert < 0) o[i] = 0.f;
-          }
-          const uint32_t off =
-              (base[fm] != kOOB && col < g.n) ? base[fm] + col * (int)sizeof(T) : kOOB;
-          llvm_amdgcn_raw_buffer_store_v2i32(
-              i32x2{(int)pack2<T>(o[0], o[1]), (int)pack2<T>(o[2], o[3])}, rC, off, 0, 0);
+        for (int j = 0; j < OF; ++j) {
+          const int col = ncol0 + wave * OF * 16 + j * 16 + grp * 4;
+          llvm_amdgcn_raw_buffer_store_v2i32(i32x2{(int)outp(j, 0), (int)outp(j, 2)}, rC,
+                                             offset(col), 0, 0);
         }
       }
     }
