@@ -474,12 +474,14 @@ def test_moe_layer_fp16_wide_routed_tiles():
 
 @pytest.mark.parametrize("m,n,k,dtype,block_m",
                          [(2300, 3072, 256, torch.float16, 128),
+                          (2300, 3068, 256, torch.bfloat16, 128),
                           (2048, 2048, 256, torch.bfloat16, 128),
                           (1200, 2048, 256, torch.float16, 64),
                           (1600, 1536, 768, torch.bfloat16, 64)])
 def test_routed_gemm_multi_round_grid(m, n, k, dtype, block_m):
     # several rounds of tiles: 68-75 routed 128-row blocks (the persistent
-    # kernel; 128 x 256 tiles at N = 3072, whose rounds are 88% full,
+    # kernel; 128 x 256 tiles at N = 3072, whose rounds are 88% full, and at
+    # N = 3068, whose rows take 8-byte stores instead of 16-byte ones;
     # 128 x 128 at N = 2048), or 83-108 blocks of 64 rows (64 x 256 tiles,
     # 3 stages).  Expert -1 blocks, ids outside [0, E) (rows left
     # untouched), route weights, per-expert scales
