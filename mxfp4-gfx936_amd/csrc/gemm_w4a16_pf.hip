@@ -1125,7 +1125,18 @@ int launch_pf_checkpoint(const GemmArgs& g, int cfg, hipStream_t st) {
     const bool dense = g.sorted_ids == nullptr;
     switch (cfg) {
       case PF_32x128:
-        if (!dense) return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4, false, 2>(g, st);
+        // 4-stage groups (128 bytes of each weight row per load) while the
+        // experts average <= 20 routes; with more, the tiles of an expert
+        // share its weights through the caches and the 2-stage groups' five
+        // workgroups per CU (three with 4-stage ones) win.  Cold weights
+        // (3 copies rotated, E=128, top-8, K=2048, N=1536): soft op at 128 /
+        // 256 / 320 tokens 65.9 / 68.5 / 69.4 -> 60.0 / 62.2 / 63.1 us,
+        // 384 70.98 vs 72.84 (kept 2-stage); MoE layer 128-320 tokens -5 us
+        if (!dense) {
+          if ((int64_t)g.num_valid <= 20 * (int64_t)g.num_experts)
+            return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4, false, 4>(g, st);
+          return launch_cfg<T, 1, 4, 2, 2, 3, EPI, 4, false, 2>(g, st);
+        }
         break;
       case PF_32x256:
         if (!dense) return launch_cfg<T, 1, 4, 2, 4, 3, EPI, 3, false, 2>(g, st);

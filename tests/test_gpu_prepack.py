@@ -169,21 +169,23 @@ def test_registered_dense_copy_serves_the_reference_signature():
         P.unregister_prepacked(w)
 
 
-def test_routed_32x256_line_groups_bitwise():
-    # AITER's entry with BLOCK_SIZE_M 32 at 1024 tokens, E=128, top-8: more
-    # than ten 32 x 128 tiles per CU, so the checkpoint layout runs 32 x 256
-    # tiles with 2-stage weight-line groups; the registered prepacked copy
-    # runs its own 32-row tiles; bitwise the same C, and sampled rows on the
-    # FP64 oracle
+# AITER's entry with BLOCK_SIZE_M 32, E=128, top-8.  1024 tokens: more than
+# ten 32 x 128 tiles per CU, so the checkpoint layout runs 32 x 256 tiles
+# with 2-stage weight-line groups; 256 tokens (16 routes per expert): 32 x
+# 128 tiles with 4-stage groups.  The registered prepacked copy runs its own
+# 32-row tiles; bitwise the same C, and sampled rows on the FP64 oracle
+@pytest.mark.parametrize("m", [1024, 256])
+def test_routed_32x256_line_groups_bitwise(m):
     from mxfp4_amd import prepack as P
     from oracle import mxfp4_oracle as O
     from _helpers import assert_parity
-    rng = np.random.default_rng(1024)
-    m, e, top_k, k, n = 1024, 128, 8, 2048, 1536
+    print(f"routed 32-row line groups m={m}", flush=True)
+    rng = np.random.default_rng(m)
+    e, top_k, k, n = 128, 8, 2048, 1536
     wp, ws = rand_mxfp4(rng, (e, n), k)
     B, Bs = cuda(wp), cuda(ws)
-    a = cuda(rand_act(1025, (m, k)))
-    g = torch.Generator().manual_seed(1026)
+    a = cuda(rand_act(m + 1, (m, k)))
+    g = torch.Generator().manual_seed(m + 2)
     tw, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
     tw, ids = tw.cuda(), ids.cuda()
     srt, eid, npp = mx.make_routing_device(ids, e, 32)
@@ -202,7 +204,7 @@ def test_routed_32x256_line_groups_bitwise():
         P.unregister_prepacked(B)
     torch.cuda.synchronize()
     assert torch.equal(plain, fast)
-    rows = np.arange(0, m, 53)
+    rows = np.arange(0, m, 53 if m > 512 else 13)
     oracle = O.fused_moe_fp64(a.float().cpu().numpy()[rows], wp, ws, 1.0, np.ones(e),
                               tw.cpu().numpy()[rows], ids.cpu().numpy()[rows], True)
     assert_parity(plain.float().cpu().numpy()[rows], oracle, what="routed 32 x 256 groups")
