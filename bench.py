@@ -24,8 +24,10 @@ on ``bench.py --traffic-probe`` and recorded in
 profiles/w4a16_pf_qkv_prefill_traffic.md, or null when that file is absent.  ``sweep`` carries the other BASELINE points:
 decode W4A16 GEMV (HBM GB/s, weights rotated over >= 512 MB so the 256 MB
 MALL cannot serve them, launches replayed from a HIP graph), the routed MoE
-layer (us), the soft op (C bf16 at 512 and 4096 tokens, C FP32 on the FP32
-MFMA at 512) and the AITER entry on caller metadata, W4A4 on the
+layer (us, 3 weight copies rotated), the soft op (C bf16 at 512 and 4096
+tokens, C FP32 on the FP32 MFMA at 512) and the AITER entry on caller
+metadata (3 weight copies rotated; ``us_one_copy`` replays a single copy,
+whose weights the MALL then serves), W4A4 on the
 block-scaled FP4 MFMA, and the standalone dequant.
 ``cpu_baseline`` times the reference safe path (explicit dequant +
 torch.matmul bf16, restated in oracle/) on this host's cores on a bounded
@@ -39,6 +41,7 @@ per-row time cap.
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import sys
@@ -398,13 +401,18 @@ def linear_bytes(m, n, k, prepacked=False):
     return n * k // 2 + n * k // (16 if prepacked else 32) + 2 * m * k + 2 * m * n
 
 
-def soft_op_cases(mx, torch, np):
-    """(name, call, FLOPs, peak) of the soft-op and AITER-entry rows: BASELINE
-    config 3's gate_up shape (E=128, top-8, K=2048, N=1536), seeded."""
+def soft_op_cases(mx, torch, np, copies=3):
+    """(name, calls, FLOPs, peak) of the soft-op and AITER-entry rows: BASELINE
+    config 3's gate_up shape (E=128, top-8, K=2048, N=1536), seeded.  `calls`
+    holds one call per weight copy: the 201 MB of one copy fit the 256 MB
+    MALL, so replaying a single copy would time MALL-resident weights, where
+    a serving step finds a layer's weights in HBM."""
     e, k, n, top_k = 128, 2048, 1536, 8
-    (wp, wsc), = rand_weights(np.random.default_rng(20260818), (e, n), k)
+    rng = np.random.default_rng(20260818)
+    wcs = rand_weights(rng, (e, n), k, copies)
     one, ones_e, empty = (torch.ones(1, device="cuda"), torch.ones(e, device="cuda"),
                           torch.empty(0, device="cuda"))
+    regs = []
     cases = []
     for m, cdt, name in ((512, torch.bfloat16, "bf16"), (4096, torch.bfloat16, "bf16"),
                          (512, torch.float32, "f32")):
@@ -415,54 +423,64 @@ def soft_op_cases(mx, torch, np):
         C = torch.empty((m, top_k, n), dtype=cdt, device="cuda")
         fl = 2.0 * m * top_k * n * k
         peak = FP32_PEAK_TFLOPS if cdt == torch.float32 else BF16_PEAK_TFLOPS
-        cases.append((f"fused_moe_soft_c{name}_m{m}",
-                      lambda a=a, C=C, tw=tw, ids=ids: mx.fused_moe_mxfp4_soft(
-                          a, wp, C, one, ones_e, None, wsc, tw, ids, empty, empty, empty, True,
-                          top_k, False, False), fl, peak))
+
+        def soft(ws, a=a, C=C, tw=tw, ids=ids):
+            return [lambda wp=wp, wsc=wsc: mx.fused_moe_mxfp4_soft(
+                a, wp, C, one, ones_e, None, wsc, tw, ids, empty, empty, empty, True, top_k,
+                False, False) for wp, wsc in ws]
+
+        def aiter(ws, bm, a=a, C=C, tw=tw, ids=ids):
+            srt, eid, npp = mx.make_routing_device(ids, e, bm)
+            return [lambda wp=wp, wsc=wsc: mx.fused_moe_mxfp4(
+                a, wp, C, one, ones_e, None, wsc, tw, ids, srt, eid, npp, True, top_k, False,
+                False, {"BLOCK_SIZE_M": bm}, torch.bfloat16) for wp, wsc in ws]
+
+        cases.append((f"fused_moe_soft_c{name}_m{m}", soft(wcs), fl, peak))
         if m == 512 and cdt == torch.bfloat16:
             for bm in (32, 64):
-                srt, eid, npp = mx.make_routing_device(ids, e, bm)
-                cases.append((f"aiter_fused_moe_bm{bm}_m{m}",
-                              lambda a=a, C=C, tw=tw, ids=ids, srt=srt, eid=eid, npp=npp, bm=bm:
-                              mx.fused_moe_mxfp4(a, wp, C, one, ones_e, None, wsc, tw, ids, srt,
-                                                 eid, npp, True, top_k, False, False,
-                                                 {"BLOCK_SIZE_M": bm}, torch.bfloat16),
-                              fl, BF16_PEAK_TFLOPS))
+                cases.append((f"aiter_fused_moe_bm{bm}_m{m}", aiter(wcs, bm), fl,
+                              BF16_PEAK_TFLOPS))
         if cdt == torch.bfloat16:
-            # the same calls with a registered prepacked copy of B (a second
-            # weight tensor, so the rows above keep the checkpoint layout)
-            if not any(c[0].endswith("_registered") for c in cases):
-                wp_r, wsc_r = wp.clone(), wsc.clone()
-                mx.register_prepacked(wp_r, wsc_r)
-            cases.append((f"fused_moe_soft_c{name}_m{m}_registered",
-                          lambda a=a, C=C, tw=tw, ids=ids: mx.fused_moe_mxfp4_soft(
-                              a, wp_r, C, one, ones_e, None, wsc_r, tw, ids, empty, empty, empty,
-                              True, top_k, False, False), fl, peak))
+            # the same calls with a registered prepacked copy of B (second
+            # weight tensors, so the rows above keep the checkpoint layout)
+            if not regs:
+                for wp, wsc in wcs:
+                    wp_r, wsc_r = wp.clone(), wsc.clone()
+                    mx.register_prepacked(wp_r, wsc_r)
+                    regs.append((wp_r, wsc_r))
+            cases.append((f"fused_moe_soft_c{name}_m{m}_registered", soft(regs), fl, peak))
             if m == 512:
-                srt, eid, npp = mx.make_routing_device(ids, e, 64)
-                cases.append((f"aiter_fused_moe_bm64_m{m}_registered",
-                              lambda a=a, C=C, tw=tw, ids=ids, srt=srt, eid=eid, npp=npp:
-                              mx.fused_moe_mxfp4(a, wp_r, C, one, ones_e, None, wsc_r, tw, ids,
-                                                 srt, eid, npp, True, top_k, False, False,
-                                                 {"BLOCK_SIZE_M": 64}, torch.bfloat16),
-                              fl, BF16_PEAK_TFLOPS))
+                cases.append((f"aiter_fused_moe_bm64_m{m}_registered", aiter(regs, 64), fl,
+                              BF16_PEAK_TFLOPS))
     return cases
 
 
 def soft_probe() -> int:
     """Soft-op and AITER-entry launches for trace runs (the soft_op_cases
-    rows), each after an untimed clock ramp, 20 calls."""
+    rows): per row an untimed clock ramp and 20 timed calls, both over the
+    rotated weight copies, then a one-element fill kernel as the row's end
+    marker."""
     import numpy as np
     import torch
 
     import mxfp4_amd as mx
     mx._lib.load()
-    for key, fn, _, _ in soft_op_cases(mx, torch, np):
-        ramp_clocks(fn)
-        for _ in range(20):
-            fn()
+    for key, fns, _, _ in soft_op_cases(mx, torch, np):
+        # the ramp rotates the copies too: after a ramp on one (MALL-served)
+        # copy the rotated calls of the prepacked rows ran 8-10 us slower
+        rot = itertools.cycle(fns)
+        ramp_clocks(lambda: next(rot)())
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(20):
+            fns[i % len(fns)]()
+        end.record()
+        # a one-element fill marks the end of the case's launches in a trace
+        torch.full((1,), 0.0, device="cuda")
         torch.cuda.synchronize()
-        log(f"soft probe {key} done")
+        log(f"soft probe {key}: {start.elapsed_time(end) * 1e3 / 20:.2f} us per call "
+            "(20 calls over the rotated copies)")
     print(json.dumps({"probe": "soft"}))
     return 0
 
@@ -549,12 +567,15 @@ def sweep(mx, torch, np):
     # (aiter:367-472) on caller metadata of BLOCK_SIZE_M 32 and 64 at 512
     # tokens (the metadata is built once, outside the timing, as a caller
     # would pass it in).
-    for key, fn, fl, peak in soft_op_cases(mx, torch, np):
-        t = time_graph([fn] * 4, replays=10)
-        te = time_eager(fn, 20, 3)[1]
+    for key, fns, fl, peak in soft_op_cases(mx, torch, np):
+        t = time_graph(fns, replays=10)
+        t1 = time_graph([fns[0]] * len(fns), replays=10)
+        rot = itertools.cycle(fns)
+        te = time_eager(lambda: next(rot)(), 21, 3)[1]
         res[key] = {"us": round(t * 1e3, 2), "TFLOP/s": round(fl / t / 1e9, 2),
                     "peak_frac": round(fl / t / 1e9 / peak, 4), "peak": peak,
-                    "eager_us": round(te * 1e3, 2)}
+                    "eager_us": round(te * 1e3, 2), "weight_copies": len(fns),
+                    "us_one_copy": round(t1 * 1e3, 2)}
         log(f"{key}: {res[key]}")
     torch.cuda.empty_cache()
     # --- W4A4, activations/weights quantized with the RNE rule
