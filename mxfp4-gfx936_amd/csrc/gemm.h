@@ -17,6 +17,7 @@ enum Epilogue {
   EPI_STORE = 0,     // c = T(acc * alpha [* route_w] [+ bias])
   EPI_SILU_MUL = 1,  // gate/up column pairs -> h = silu(g) * u, rounded like vllm:249-252
   EPI_PARTIAL = 2,   // FP32 partial sums of one K slice (split K, dense only)
+  EPI_STORE_F32 = 3, // c = float(acc * alpha [* route_w] [+ bias]): bf16 A, C in FP32 (prefill tiles)
 };
 
 struct GemmArgs {

@@ -1012,6 +1012,16 @@ int launch_typed(const GemmArgs& g, hipStream_t st) {
 }  // namespace
 
 int launch_w4a16(const GemmArgs& g, int dtype, int epi, hipStream_t st) {
+  if (epi == EPI_STORE_F32) {
+    // bf16 A, C in FP32: routed blocks of a multiple of 32 rows on the
+    // prefill tiles only (the other kernels store T)
+    if (dtype != MXFP4_DT_BF16 || g.route_ids || !g.sorted_ids || g.block_m % 32 != 0 ||
+        !pf_supported(g, 2)) {
+      set_error("w4a16: C in FP32 needs bf16 activations on routed blocks of 32k rows");
+      return MXFP4_ERR_VALUE;
+    }
+    return launch_w4a16_pf(g, MXFP4_DT_BF16, EPI_STORE_F32, pf_choose(g, EPI_STORE), st);
+  }
   if (dtype == MXFP4_DT_BF16)
     return epi == EPI_STORE ? launch_typed<__bf16, EPI_STORE>(g, st)
                             : launch_typed<__bf16, EPI_SILU_MUL>(g, st);

@@ -216,8 +216,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
     for (int idx = tid; idx < BM * OUT_COLS; idx += NT) {
       const int r = idx / OUT_COLS, cc = idx % OUT_COLS;
       const RowInfo ri = row_info(g, pos0 + r);
-      if (ri.valid && ncol0 + cc < g.n)
-        static_cast<T*>(g.c)[ri.out_row * g.ldc + ncol0 + cc] = from_f32<T>(0.f);
+      if (ri.valid && ncol0 + cc < g.n) {
+        if constexpr (EPI == EPI_STORE_F32)
+          static_cast<float*>(g.c)[ri.out_row * g.ldc + ncol0 + cc] = 0.f;
+        else
+          static_cast<T*>(g.c)[ri.out_row * g.ldc + ncol0 + cc] = from_f32<T>(0.f);
+      }
     }
     return;
   }
@@ -440,10 +444,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   // after the slices are summed
   const float alpha = (EPI == EPI_PARTIAL) ? 1.0f : scalar_alpha(g, expert);
   // the lane's bias values, once (columns past N read as zero)
-  float bv[EPI == EPI_STORE ? FN : 1][4];
-  if (EPI == EPI_STORE && g.bias) {
+  constexpr bool kBias = EPI == EPI_STORE || EPI == EPI_STORE_F32;
+  float bv[kBias ? FN : 1][4];
+  if (kBias && g.bias) {
 #pragma unroll
-    for (int fn = 0; fn < (EPI == EPI_STORE ? FN : 1); ++fn) {
+    for (int fn = 0; fn < (kBias ? FN : 1); ++fn) {
       const int col = ncol0 + wn * FN * 16 + fn * 16 + grp * 4;
       const T* bp = static_cast<const T*>(g.bias) + col;
       if (col + 4 <= g.n && (reinterpret_cast<uintptr_t>(bp) & 7) == 0) {
@@ -457,6 +462,38 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
         for (int i = 0; i < 4; ++i) bv[fn][i] = col + i < g.n ? to_f32(bp[i]) : 0.f;
       }
     }
+  }
+  if constexpr (EPI == EPI_STORE_F32) {
+    // C in FP32: a lane's 4 consecutive columns of a fragment are one
+    // 16-byte store, nothing rounded to T (the products of bf16 A and the
+    // E2M1 x 2^k weights are exact, summed in FP32 by the MFMA)
+    float* const cbase = static_cast<float*>(g.c);
+    const bool vec = g.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(g.c) & 15) == 0;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const RowInfo r = row_info(g, pos0 + wm * FM * 16 + fm * 16 + c16);
+      if (!r.valid) continue;
+      const float rw = g.route_w ? g.route_w[r.out_row] : 1.0f;
+      float* const crow = cbase + r.out_row * g.ldc;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int col = ncol0 + wn * FN * 16 + fn * 16 + grp * 4;
+        if (col >= g.n) continue;
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o[i] = acc[fm][fn][i] * alpha;
+          if (g.route_w) o[i] *= rw;
+          if (g.bias) o[i] += bv[fn][i];
+        }
+        if (vec && col + 4 <= g.n) {
+          *reinterpret_cast<f32x4*>(crow + col) = f32x4{o[0], o[1], o[2], o[3]};
+        } else {
+          for (int i = 0; i < 4 && col + i < g.n; ++i) crow[col + i] = o[i];
+        }
+      }
+    }
+    return;
   }
   if constexpr (EPI == EPI_STORE && FN >= 2) {
     if (g.ldc % 8 == 0) {
@@ -1009,8 +1046,8 @@ int launch_cfg(const GemmArgs& g, hipStream_t st) {
     set_error("w4a16 prefill: bad grid");
     return MXFP4_ERR_VALUE;
   }
-  if constexpr (BGV == 1 && EPI != EPI_PARTIAL && WGM == 1 && WGN == 4 && STAGES == 2 &&
-                FN <= 4) {
+  if constexpr (BGV == 1 && EPI != EPI_PARTIAL && EPI != EPI_STORE_F32 && WGM == 1 &&
+                WGN == 4 && STAGES == 2 && FN <= 4) {
     // routed grid of more tiles than resident workgroups: the persistent
     // kernel (dense grids run 2-5% slower in it: their tiles start with
     // one load round trip, not the routed two, and gain nothing)
@@ -1334,8 +1371,13 @@ int launch_w4a16_pf(const GemmArgs& g, int dtype, int epi, int cfg, hipStream_t 
     switch (epi) {
       case EPI_STORE: return launch_pf_layout<__bf16, EPI_STORE>(g, cfg, st);
       case EPI_PARTIAL: return launch_pf_layout<__bf16, EPI_PARTIAL>(g, cfg, st);
+      case EPI_STORE_F32: return launch_pf_layout<__bf16, EPI_STORE_F32>(g, cfg, st);
       default: return launch_pf_layout<__bf16, EPI_SILU_MUL>(g, cfg, st);
     }
+  }
+  if (epi == EPI_STORE_F32) {
+    set_error("w4a16 prefill: C in FP32 takes bf16 activations only");
+    return MXFP4_ERR_TYPE;
   }
   switch (epi) {
     case EPI_STORE: return launch_pf_layout<_Float16, EPI_STORE>(g, cfg, st);

@@ -645,6 +645,13 @@ int dispatch_gemm(const GemmArgs& g, int a_dtype, int c_dtype, int epi, hipStrea
       set_error("the FP32 compute path supports the plain epilogue only");
       return MXFP4_ERR_TYPE;
     }
+    // bf16 A on routed blocks of 32k rows: the bf16 MFMA's products of A and
+    // the E2M1 x 2^k weights (exact in bf16) are exact and summed in FP32,
+    // the FP32 GEMM's arithmetic up to the summation order; the W4A16 prefill
+    // tiles then store FP32.  Other A types and block sizes: the FP32 MFMA.
+    if (a_dtype == MXFP4_DT_BF16 && g.sorted_ids && !g.route_ids && g.block_m % 32 == 0 &&
+        pf_supported(g, 2))
+      return launch_w4a16(g, MXFP4_DT_BF16, EPI_STORE_F32, st);
     return launch_f32_reference(g, a_dtype, st);
   }
   if (a_dtype != c_dtype) {
@@ -831,13 +838,18 @@ enum SoftPath {
   SOFT_W4A16,      // bf16 / fp16 A and C, checkpoint-layout weights
   SOFT_W4A16_PRE,  // the same with a prepacked copy
   SOFT_SCALED,     // packed MXFP4 / FP8 A on the block-scaled MFMA
-  SOFT_F32,        // C in FP32
+  SOFT_F32,        // C in FP32, fp16 / fp32 A (FP32 MFMA)
+  SOFT_F32_W4A16,  // C in FP32, bf16 A: the W4A16 prefill tiles storing FP32
+  SOFT_F32_W4A16_PRE,
 };
 
 SoftPath soft_path(int a_dtype, int c_dtype, bool prepacked) {
   if (a_dtype == MXFP4_DT_U8 || a_dtype == MXFP4_DT_F8E4M3 || a_dtype == MXFP4_DT_F8E5M2)
     return SOFT_SCALED;
-  if (c_dtype == MXFP4_DT_F32) return SOFT_F32;
+  if (c_dtype == MXFP4_DT_F32) {
+    if (a_dtype != MXFP4_DT_BF16) return SOFT_F32;
+    return prepacked ? SOFT_F32_W4A16_PRE : SOFT_F32_W4A16;
+  }
   return prepacked ? SOFT_W4A16_PRE : SOFT_W4A16;
 }
 
@@ -853,6 +865,12 @@ SoftPath soft_path(int a_dtype, int c_dtype, bool prepacked) {
 // 75.0 / 73.4 / 73.4 / 91.7 vs 73.9 / 76.9 / 79.4 / 88.1.  The packed /
 // FP8 path keeps 32 up to 32 routes per expert, else 64.
 int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path, int64_t k) {
+  if (path == SOFT_F32_W4A16 || path == SOFT_F32_W4A16_PRE) {
+    // the W4A16 rule, at least 32 rows (the prefill tiles)
+    const int b = soft_block_m(routes, num_experts,
+                               path == SOFT_F32_W4A16 ? SOFT_W4A16 : SOFT_W4A16_PRE, k);
+    return b < 32 ? 32 : b;
+  }
   const double avg = (double)routes / (double)(num_experts > 0 ? num_experts : 1);
   if (avg <= 1.5) return 16;
   if (path == SOFT_F32) return avg <= 8.0 ? 16 : 32;

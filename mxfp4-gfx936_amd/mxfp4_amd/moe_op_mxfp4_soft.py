@@ -302,7 +302,12 @@ def _prepare_moe_operands(A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, top
             raise ValueError("unpacked activations must not provide A_mx_scale")
         if A.ndim != 2 or A.shape[1] != logical_k:
             raise RuntimeError(f"activations must be [M, {logical_k}], got {tuple(A.shape)}")
-        act = A if A.dtype == matmul_dtype else A.to(matmul_dtype)
+        # soft:475 converts A to the compute dtype; with C in FP32, bf16 and
+        # fp16 A go in as they are, and the kernels widen them exactly
+        # (bf16 A: the W4A16 prefill tiles storing FP32; fp16: the FP32 MFMA)
+        keep = A.dtype == matmul_dtype or (matmul_dtype == torch.float32
+                                           and A.dtype in (torch.bfloat16, torch.float16))
+        act = A if keep else A.to(matmul_dtype)
         act = _lib.aligned(act)
         act_mx = None
     m = topk_ids.shape[0]

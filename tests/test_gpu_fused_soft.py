@@ -266,6 +266,54 @@ def test_soft_op_fp32_stage_counts(k, m, e, top_k, n):
     assert_parity(out, oracle, what=f"fp32 k={k} m={m} n={n}")
 
 
+# C in FP32 with bf16 activations: routing blocks of 32 / 64 / 128 rows run
+# the W4A16 prefill tiles storing FP32 (the bf16 MFMA's products of bf16 A
+# and the E2M1 x 2^k weights are exact, summed in FP32); the same values as
+# FP32 A run the FP32 MFMA.  AITER's entry on caller metadata (an expert -1
+# block writes zeros, dropped routes stay untouched) and the soft op; both
+# paths on the FP64 oracle and within FP32 summation noise of each other
+@pytest.mark.parametrize("block_m", [32, 64, 128])
+def test_fp32_c_bf16_activations_prefill_tiles(block_m):
+    print(f"fp32 C, bf16 A, block {block_m}", flush=True)
+    rng = np.random.default_rng(700 + block_m)
+    m, e, top_k, k, n = 384, 16, 4, 1024, 200
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    a = rand_act(701 + block_m, (m, k))
+    w, ids = _route_with_dropped(m, e, top_k, 702 + block_m, 9)
+    ids_np = ids.numpy()
+    srt, eid, npp = O.make_routing(ids_np, block_m=block_m, num_experts=e)
+    eid = eid.copy()
+    eid[eid == 5] = -1
+
+    def aiter(act):
+        C = torch.full((m, top_k, n), 3.0, dtype=torch.float32, device="cuda")
+        mx.fused_moe_mxfp4(cuda(act), cuda(wp), C, torch.full((1,), 0.75, device="cuda"),
+                           torch.ones(e, device="cuda"), None, cuda(ws), cuda(w), cuda(ids),
+                           cuda(srt), cuda(eid), cuda(npp), True, top_k, False, False,
+                           {"BLOCK_SIZE_M": block_m}, torch.float32)
+        return C.cpu().numpy()
+
+    got, ref32 = aiter(a), aiter(a.float())
+    oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 0.75, np.ones(e), w.numpy(), ids_np,
+                              True, compute_dtype="f32")
+    dropped = (ids_np < 0) | (ids_np >= e)
+    assert np.all(got[dropped] == 3.0) and np.all(got[ids_np == 5] == 0)
+    oracle[ids_np == 5] = 0.0
+    oracle[dropped] = 3.0
+    assert_parity(got, oracle, what=f"bf16 A, C fp32, block {block_m}")
+    assert_parity(ref32, oracle, what=f"fp32 A, C fp32, block {block_m}")
+    scale = np.abs(oracle[~dropped]).max()
+    assert np.abs(got - ref32).max() <= 1e-5 * scale
+    if block_m == 32:
+        # the soft op (device routing) on the same inputs
+        soft = _run(a, None, wp, ws, ids, w, torch.float32, True).cpu().numpy()
+        assert np.all(soft[dropped] == 0)
+        soft_oracle = O.fused_moe_fp64(a.float().numpy(), wp, ws, 0.75, np.ones(e), w.numpy(),
+                                       ids_np, True, compute_dtype="f32")
+        soft_oracle[dropped] = 0.0
+        assert_parity(soft, soft_oracle, what="soft op, bf16 A, C fp32")
+
+
 @pytest.mark.parametrize("ids_dtype", [torch.int32, torch.int64])
 @pytest.mark.parametrize("m,top_k", [(1, 8), (3, 4), (8, 8)])
 def test_soft_op_direct_routing_writes_dropped_rows(m, top_k, ids_dtype):
