@@ -192,7 +192,10 @@ int mxfp4_moe_route(const float* logits, int64_t m, int num_experts, int64_t row
  *      exact, FP32 accumulation.
  *   b u8 [num_experts, n, k/2], b_mx u8 [num_experts, n, k/32], contiguous.
  *   c: output rows indexed by route id, c + route * c_row_stride, of c_dtype
- *      (BF16, F16 or F32; the compute type of soft:405-407).
+ *      (BF16, F16 or F32; the compute type of soft:405-407).  BF16 / F16 A
+ *      must match c_dtype, except with F32 c, where they are widened
+ *      exactly (BF16 A on blocks of 32k rows: the bf16 MFMA's exact
+ *      products, FP32 sums; otherwise the FP32 MFMA).
  *   For each block i < num_post_padded[0] / block_m with expert
  *   e = expert_ids[i] and each route r = sorted_ids[i*block_m + j] <
  *   num_valid:  c[r, :] = a[r / top_k] . dequant(b[e])^T * a_scale[0] *
