@@ -184,18 +184,20 @@ def test_soft_op_triton_backend_uses_caller_metadata(block_m, monkeypatch):
 # the checkpoint layout, 64 with a copy); N 200 leaves a ragged 16-row group
 @pytest.mark.parametrize("m,e,top_k,n", [(64, 16, 4, 192), (512, 16, 4, 200)],
                          ids=["blk32", "blk128"])
-@pytest.mark.parametrize("c_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("c_dtype", [torch.bfloat16, torch.float16, torch.float32],
+                         ids=["bf16", "f16", "f32"])
 def test_registered_copy_is_bitwise_the_checkpoint_result(m, e, top_k, n, c_dtype, monkeypatch):
     # a registered prepacked copy of B is read by the soft op (device
     # routing), its triton-backend value (caller metadata) and AITER's entry;
-    # each C equals the unregistered call's bit for bit
+    # each C equals the unregistered call's bit for bit (C in FP32: bf16 A on
+    # the W4A16 tiles storing FP32)
     from mxfp4_amd import prepack as P
     print(f"registered copy m={m} e={e} n={n} {c_dtype}", flush=True)
     rng = np.random.default_rng(3 * m + n)
     k = 512
     wp, ws = rand_mxfp4(rng, (e, n), k)
     B, Bs = cuda(wp), cuda(ws)
-    A = cuda(rand_act(m + 77, (m, k))).to(c_dtype)
+    A = cuda(rand_act(m + 77, (m, k))).to(torch.bfloat16 if c_dtype == torch.float32 else c_dtype)
     w, ids = _route_with_dropped(m, e, top_k, 4000 + m, 11)
     w, ids = cuda(w), cuda(ids)
     a_scale = torch.tensor([0.75], device="cuda")
