@@ -271,10 +271,12 @@ def test_soft_op_fp32_stage_counts(k, m, e, top_k, n):
 # C in FP32 with bf16 activations: routing blocks of 32 / 64 / 128 rows run
 # the W4A16 prefill tiles storing FP32 (the bf16 MFMA's products of bf16 A
 # and the E2M1 x 2^k weights are exact, summed in FP32); the same values as
-# FP32 A run the FP32 MFMA.  AITER's entry on caller metadata (an expert -1
-# block writes zeros, dropped routes stay untouched) and the soft op; both
-# paths on the FP64 oracle and within FP32 summation noise of each other
-@pytest.mark.parametrize("block_m", [32, 64, 128])
+# FP32 A run the FP32 MFMA, and so do 16-row blocks, where bf16 A is widened
+# on the way in (bitwise the FP32-A result).  AITER's entry on caller
+# metadata (an expert -1 block writes zeros, dropped routes stay untouched)
+# and the soft op; both paths on the FP64 oracle and within FP32 summation
+# noise of each other
+@pytest.mark.parametrize("block_m", [16, 32, 64, 128])
 def test_fp32_c_bf16_activations_prefill_tiles(block_m):
     print(f"fp32 C, bf16 A, block {block_m}", flush=True)
     rng = np.random.default_rng(700 + block_m)
@@ -306,6 +308,8 @@ def test_fp32_c_bf16_activations_prefill_tiles(block_m):
     assert_parity(ref32, oracle, what=f"fp32 A, C fp32, block {block_m}")
     scale = np.abs(oracle[~dropped]).max()
     assert np.abs(got - ref32).max() <= 1e-5 * scale
+    if block_m == 16:
+        assert np.array_equal(got, ref32)
     if block_m == 32:
         # the soft op (device routing) on the same inputs
         soft = _run(a, None, wp, ws, ids, w, torch.float32, True).cpu().numpy()
