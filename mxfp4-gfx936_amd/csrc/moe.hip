@@ -866,7 +866,12 @@ SoftPath soft_path(int a_dtype, int c_dtype, bool prepacked) {
 // FP8 path keeps 32 up to 32 routes per expert, else 64.
 int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path, int64_t k) {
   if (path == SOFT_F32_W4A16 || path == SOFT_F32_W4A16_PRE) {
-    // the W4A16 rule, at least 32 rows (the prefill tiles)
+    // the W4A16 rule, at least 32 rows (the prefill tiles); on the
+    // checkpoint layout 32 rows up to 32 routes per expert (C in FP32 moves
+    // twice the output bytes: the soft op at 512 tokens, 32 routes per
+    // expert, 81 us on 32-row blocks against 90 us on 64)
+    const double avg = (double)routes / (double)(num_experts > 0 ? num_experts : 1);
+    if (path == SOFT_F32_W4A16 && avg > 1.5 && avg <= 32.0) return 32;
     const int b = soft_block_m(routes, num_experts,
                                path == SOFT_F32_W4A16 ? SOFT_W4A16 : SOFT_W4A16_PRE, k);
     return b < 32 ? 32 : b;
@@ -887,11 +892,12 @@ int soft_block_m(int64_t routes, int64_t num_experts, SoftPath path, int64_t k) 
   // (AITER's entry, 64 / 128 / 256 routes per expert, 64 vs 128 rows: K=768
   // N=2048 46.8 / 75.5 / 130.9 vs 50.6 / 79.0 / 132.5 us; K=2048 N=1536
   // 84.1 / 129.7 / 235.6 vs 80.8 / 129.0 / 229.5)
-  // (32 rows up to 32 routes per expert: with the weight-line groups, on
-  // cold weights -- graph replays over 3 copies -- 32 vs 64 rows at 24 / 32
-  // / 40 routes per expert: K=2048 64.0 / 72.7 / 78.6 vs 72.6 / 76.1 / 73.3
-  // us, K=768 36.9 / 39.9 / 47.4 vs 40.1 / 40.7 / 42.3)
-  return avg <= 32.0 ? 32 : (avg <= 56.0 || k < 2048 ? 64 : 128);
+  // (32 rows up to 32 routes per expert, 30 where K >= 2048: on cold
+  // weights -- graph replays over 3 copies -- 32 vs 64 rows at 24 / 32 / 40
+  // routes per expert: K=768 36.9 / 39.9 / 47.4 vs 40.1 / 40.7 / 42.3 us;
+  // K=2048 with the register epilogues, at 20 / 24 / 28 / 32 / 36 routes:
+  // 63.3 / 71.0 / 74.9 / 80.1 / 88.0 vs 74.9 / 76.7 / 77.6 / 78.5 / 81.0)
+  return avg <= (k >= 2048 ? 30.0 : 32.0) ? 32 : (avg <= 56.0 || k < 2048 ? 64 : 128);
 }
 
 struct SoftPlan {
