@@ -69,8 +69,10 @@ def moe_weights():
 
 
 # 4096 tokens: persistent routed kernel for gate_up, 128 x 320 for down;
-# 512: one round of tiles; 4: the direct-routed decode path (copies unused)
-@pytest.mark.parametrize("m", [4096, 512, 4])
+# 512: one round of tiles; 64 (16 routes per expert over the 32 experts):
+# 32-row blocks, whose checkpoint-layout tiles take 4-stage weight-line
+# groups; 4: the direct-routed decode path (copies unused)
+@pytest.mark.parametrize("m", [4096, 512, 64, 4])
 @pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32])
 def test_moe_layer_prepacked_bitwise(m, ids_dtype, moe_weights):
     print(f"moe layer prepacked m={m} ids={ids_dtype}", flush=True)
