@@ -686,7 +686,9 @@ LayerPlan plan_layer(int64_t m, int top_k, int num_experts, int64_t hidden, int6
   // expert, 32 (32 x 256 tiles) up to ~32, 64 (64 x 256 tiles) above.
   // E.g. 96 tokens 93.6 us with 16 vs 78.4 us with 32; 448 tokens 102.3 us
   // with 64 vs 96.6 us with 32; 640 tokens 112.3 us with 64 vs 117.3 us
-  // with 32.  Against 128-row blocks (persistent 128 x 256 tiles, whose
+  // with 32 (re-measured with the register epilogues, 3 weight copies
+  // rotated, 32 vs 64 rows: 448 / 512 / 576 tokens 95.1 / 96.3 / 121.0 vs
+  // 98.7 / 101.0 / 104.2 us).  Against 128-row blocks (persistent 128 x 256 tiles, whose
   // fixed rounds of 512 workgroups quantize): 2048 tokens 236 -> 224 us,
   // 4096 385 -> 372 us, 6144 559 -> 521 us, 16384 1289 -> 1283 us; 128 rows
   // win only where their tiles just fill whole rounds (1536 tokens 166 vs
