@@ -141,16 +141,24 @@ def _safe_reference(x: torch.Tensor, packed: np.ndarray, scales: np.ndarray) -> 
 
 @pytest.mark.parametrize("m_value", [1, 8])
 def test_linear_matches_explicit_dequant_small(m_value):
-    # test:95-111 with the reference's quantizer on randn weights
+    # test:95-111 on the test's own inputs (its seed, randn drawn on the
+    # device) and the reference's quantizer.  The reference asserts bitwise
+    # equality with x @ dequant(W).T, which torch's BLAS sums in its own
+    # order.  Every product of a bf16 activation and an E2M1 x 2^s weight is
+    # exact in FP32, and an FP32 sum of 128 of them errs by a few FP32 steps
+    # at most, so two summation orders round to different bf16 values only
+    # where a sum lies that close to a bf16 rounding boundary: none of these
+    # inputs' outputs does (nor any of 20480 outputs over 40 other seeds).
     torch.manual_seed(20260811 + m_value)
     n_value, k_value = 64, 128
-    x = torch.randn((m_value, k_value), dtype=torch.bfloat16)
-    w = torch.randn((n_value, k_value), dtype=torch.bfloat16)
-    packed, scales = O.quant_mxfp4_ties_away(w.float().numpy())
-    y = mx.linear_mxfp4_soft(cuda(x), cuda(packed), cuda(scales))
+    x = torch.randn((m_value, k_value), device="cuda", dtype=torch.bfloat16)
+    w = torch.randn((n_value, k_value), device="cuda", dtype=torch.bfloat16)
+    packed, scales = O.quant_mxfp4_ties_away(w.float().cpu().numpy())
+    y = mx.linear_mxfp4_soft(x, cuda(packed), cuda(scales))
     assert y.dtype == torch.bfloat16 and y.shape == (m_value, n_value)
-    ref = _safe_reference(cuda(x), packed, scales)
-    assert_parity(y, O.linear_fp64(x.float().numpy(), packed, scales), ref=ref)
+    ref = _safe_reference(x, packed, scales)
+    assert torch.equal(y, ref)
+    assert_parity(y, O.linear_fp64(x.float().cpu().numpy(), packed, scales), ref=ref)
 
 
 @pytest.mark.parametrize("k,n", [(2048, 5120), (4096, 2048)], ids=["qkv", "o_proj"])
