@@ -210,3 +210,43 @@ def test_routed_32x256_line_groups_bitwise(m):
     oracle = O.fused_moe_fp64(a.float().cpu().numpy()[rows], wp, ws, 1.0, np.ones(e),
                               tw.cpu().numpy()[rows], ids.cpu().numpy()[rows], True)
     assert_parity(plain.float().cpu().numpy()[rows], oracle, what="routed 32 x 256 groups")
+
+
+# 4-stage weight-line groups whose last group is half past the end of K
+# (K / 64 = 6 or 10 stages: the last group's load covers two stages that do
+# not exist, reading the next row's bytes or zeros past the buffer, which no
+# stage uses) and a ragged last column tile (N = 200): 12.5 routes per
+# expert on 32-row blocks take the 32 x 128 tiles with 4-stage groups
+@pytest.mark.parametrize("k", [384, 640])
+def test_routed_line_groups_partial_last_group(k):
+    from mxfp4_amd import prepack as P
+    from oracle import mxfp4_oracle as O
+    from _helpers import assert_parity
+    print(f"routed 4-stage line groups k={k}", flush=True)
+    rng = np.random.default_rng(k)
+    m, e, top_k, n = 100, 16, 2, 200
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    B, Bs = cuda(wp), cuda(ws)
+    a = cuda(rand_act(k + 1, (m, k)))
+    g = torch.Generator().manual_seed(k + 2)
+    tw, ids = torch.topk(torch.softmax(torch.randn((m, e), generator=g), -1), top_k, dim=-1)
+    tw, ids = tw.cuda(), ids.cuda()
+    srt, eid, npp = mx.make_routing_device(ids, e, 32)
+    one, ones_e = torch.ones(1, device="cuda"), torch.ones(e, device="cuda")
+
+    def run():
+        C = torch.full((m, top_k, n), 3.0, dtype=torch.bfloat16, device="cuda")
+        mx.fused_moe_mxfp4(a, B, C, one, ones_e, None, Bs, tw, ids, srt, eid, npp, True, top_k,
+                           False, False, {"BLOCK_SIZE_M": 32}, torch.bfloat16)
+        return C
+    plain = run()
+    P.register_prepacked(B, Bs)
+    try:
+        fast = run()
+    finally:
+        P.unregister_prepacked(B)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, fast)
+    oracle = O.fused_moe_fp64(a.float().cpu().numpy(), wp, ws, 1.0, np.ones(e),
+                              tw.cpu().numpy(), ids.cpu().numpy(), True)
+    assert_parity(plain.float().cpu().numpy(), oracle, what=f"4-stage groups k={k}")
