@@ -180,6 +180,44 @@ def test_soft_op_triton_backend_uses_caller_metadata(block_m, monkeypatch):
     assert_parity(out, oracle, what=f"triton backend block {block_m}")
 
 
+def test_triton_value_matches_safe_on_the_reference_inputs(monkeypatch):
+    # test:144-213 on the test's own inputs (its seed, randn drawn on the
+    # device; the reference's quantizer): one expert, top-1, 16 tokens, the
+    # triton value fed identity metadata of one 16-row block.  The reference
+    # asserts the two values bitwise equal.  Here they take different
+    # kernels -- the safe value's device routing puts the 16 routes in a
+    # 32-row block (prefill tile, sequential K), the caller's 16-row block
+    # takes the decode kernel (K split across waves, partial sums added in
+    # a fixed order) -- so their FP32 sums of the exact products may differ
+    # by a few FP32 steps; no output of these inputs lies that close to a
+    # bf16 rounding boundary.
+    torch.manual_seed(20260812)
+    m, n, k, e, top_k = 16, 256, 2048, 1, 1
+    activations = torch.randn((m, k), device="cuda", dtype=torch.bfloat16)
+    weights = torch.randn((e, n, k), device="cuda", dtype=torch.bfloat16)
+    packed, scales = (cuda(t) for t in O.quant_mxfp4_ties_away(weights.float().cpu().numpy()))
+    tw = torch.ones((m, top_k), device="cuda", dtype=torch.float32)
+    ti = torch.zeros((m, top_k), device="cuda", dtype=torch.int64)
+    one, ones_e = torch.ones(1, device="cuda"), torch.ones(e, device="cuda")
+    empty = torch.empty(0, device="cuda", dtype=torch.int32)
+    expected = torch.empty((m, top_k, n), device="cuda", dtype=torch.bfloat16)
+    monkeypatch.setenv("MXFP4_GFX936_BACKEND", "safe")
+    mx.fused_moe_mxfp4_soft(activations, packed, expected, one, ones_e, None, scales, tw, ti,
+                            empty, empty, empty, False, top_k, False, False)
+    actual = torch.empty_like(expected)
+    monkeypatch.setenv("MXFP4_GFX936_BACKEND", "triton")
+    mx.fused_moe_mxfp4_soft(activations, packed, actual, one, ones_e, None, scales, tw, ti,
+                            torch.arange(m, device="cuda", dtype=torch.int32),
+                            torch.zeros(1, device="cuda", dtype=torch.int32),
+                            torch.tensor([m], device="cuda", dtype=torch.int32), False, top_k,
+                            False, False)
+    assert torch.equal(actual, expected)
+    oracle = O.fused_moe_fp64(activations.float().cpu().numpy(), packed.cpu().numpy(),
+                              scales.cpu().numpy(), 1.0, np.ones(e), tw.cpu().numpy(),
+                              ti.cpu().numpy(), False)
+    assert_parity(actual, oracle, what="triton vs safe, reference inputs")
+
+
 # routes per expert 16 (32-row blocks either way) and 128 (128-row blocks on
 # the checkpoint layout, 64 with a copy); N 200 leaves a ragged 16-row group
 @pytest.mark.parametrize("m,e,top_k,n", [(64, 16, 4, 192), (512, 16, 4, 200)],
