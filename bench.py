@@ -267,9 +267,10 @@ def decode_probe() -> int:
 
 
 def moe_probe() -> int:
-    """MoE layer prefill launches for trace runs of the routed GEMMs: E=128,
-    top-8, H=2048, I=768 with prepacked weights, 512 and 4096 tokens, each
-    after an untimed clock ramp, 20 launches."""
+    """MoE layer prefill launches for trace and counter runs of the routed
+    GEMMs: E=128, top-8, H=2048, I=768 with prepacked weights, 512 and 4096
+    tokens, each after an untimed clock ramp, 20 launches; then the 256 MiB
+    calibration copy of --traffic-probe (FETCH_SIZE / WRITE_SIZE scale)."""
     import numpy as np
     import torch
 
@@ -291,7 +292,13 @@ def moe_probe() -> int:
             mx.moe_layer(x, w13, s13, w2, s2, w, ids, **pre)
         torch.cuda.synchronize()
         log(f"moe probe m={m} done")
-    print(json.dumps({"probe": "moe", "m": [512, 4096]}))
+    del pre
+    a = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "moe", "m": [512, 4096], "copy_bytes": COPY_BYTES}))
     return 0
 
 
