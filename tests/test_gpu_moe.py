@@ -837,3 +837,39 @@ def test_soft_op_fp8_activations_convert_to_compute_dtype():
                                 torch.full((m, k // 32), 127, dtype=torch.uint8, device="cuda"),
                                 cuda(ws), cuda(w), cuda(ids), _empty(), _empty(), _empty(), True,
                                 top_k, False, False)
+
+
+def test_empty_token_batches():
+    # zero tokens through every entry point: the reference returns empty
+    # results (torch.matmul of [0, K]; the safe MoE loop finds no routes and
+    # leaves C as zero_() made it, soft:476-494; the layer's sum over
+    # nothing), and so must these -- no launch, no error
+    rng = np.random.default_rng(3)
+    e, top_k, k, n, inter = 4, 2, 256, 64, 64
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    B, Bs = cuda(wp), cuda(ws)
+    x = torch.empty((0, k), dtype=torch.bfloat16, device="cuda")
+    y = mx.linear_mxfp4_soft(x, B[0], Bs[0])
+    assert y.shape == (0, n) and y.dtype == torch.bfloat16
+    y3 = mx.linear_mxfp4_soft(torch.empty((2, 0, k), dtype=torch.float16, device="cuda"),
+                              B[0], Bs[0])
+    assert y3.shape == (2, 0, n) and y3.dtype == torch.float16
+    tw = torch.empty((0, top_k), dtype=torch.float32, device="cuda")
+    ti = torch.empty((0, top_k), dtype=torch.int64, device="cuda")
+    C = torch.empty((0, top_k, n), dtype=torch.bfloat16, device="cuda")
+    one, ones_e = torch.ones(1, device="cuda"), torch.ones(e, device="cuda")
+    mx.fused_moe_mxfp4_soft(x, B, C, one, ones_e, None, Bs, tw, ti, _empty(), _empty(), _empty(),
+                            True, top_k, False, False)
+    empty_i = torch.empty(0, dtype=torch.int32, device="cuda")
+    mx.fused_moe_mxfp4(x, B, C, one, ones_e, None, Bs, tw, ti, empty_i, empty_i,
+                       torch.zeros(1, dtype=torch.int32, device="cuda"), True, top_k, False, False,
+                       {"BLOCK_SIZE_M": 32}, torch.bfloat16)
+    w13p, w13s = rand_mxfp4(rng, (e, 2 * inter), k)
+    w2p, w2s = rand_mxfp4(rng, (e, k), inter)
+    out = mx.moe_layer(x, cuda(w13p), cuda(w13s), cuda(w2p), cuda(w2s), tw, ti)
+    assert out.shape == (0, k) and out.dtype == torch.bfloat16
+    rw, ri = mx.route_topk(torch.empty((0, e), device="cuda"), top_k)
+    assert rw.shape == (0, top_k) and ri.shape == (0, top_k)
+    qp, qs = mx.dynamic_mxfp4_quant(x)
+    assert qp.shape == (0, k // 2) and qs.shape == (0, k // 32)
+    torch.cuda.synchronize()
