@@ -288,6 +288,26 @@ def test_linear_pipelined_decode_grid(dt):
     assert_parity(y, oracle, ref=ref, what=f"pipelined {dt}")
 
 
+def test_linear_activations_beyond_2gib():
+    # x [270000, 4096] bf16 is 2.2 GB: past what a 32-bit buffer offset
+    # addresses, so the GEMM takes the kernel that addresses its operands
+    # with 64-bit pointers; rows near the start, the 2^31-byte mark and
+    # the end against the FP64 oracle
+    m, k, n = 270000, 4096, 128
+    rng = np.random.default_rng(2048)
+    packed, scales = rand_mxfp4(rng, (n,), k)
+    g = torch.Generator(device="cuda").manual_seed(2049)
+    x = torch.randn((m, k), generator=g, device="cuda", dtype=torch.bfloat16)
+    assert x.numel() * 2 > 1 << 31
+    y = mx.linear_mxfp4_soft(x, cuda(packed), cuda(scales))
+    rows = np.array([0, 1, (1 << 31) // (k * 2) - 1, (1 << 31) // (k * 2), m - 2, m - 1])
+    xs = x[torch.from_numpy(rows).cuda()].float().cpu().numpy()
+    oracle = O.linear_fp64(xs, packed, scales)
+    assert_parity(y[torch.from_numpy(rows).cuda()], oracle, what="2.2 GB of activations")
+    del x, y
+    torch.cuda.empty_cache()
+
+
 def test_linear_bias_and_leading_dims():
     rng = np.random.default_rng(31)
     n, k = 96, 256

@@ -180,6 +180,34 @@ def test_soft_op_triton_backend_uses_caller_metadata(block_m, monkeypatch):
     assert_parity(out, oracle, what=f"triton backend block {block_m}")
 
 
+def test_soft_op_activations_beyond_2gib():
+    # A [270000, 4096] bf16 (2.2 GB) routed top-1 over 2 experts: the
+    # routed GEMM on the kernel with 64-bit operand addressing, and the
+    # routing over 264 chunks of 1024 routes (the separate scan and
+    # placement launches beyond 64 chunks); sampled rows near the start,
+    # the 2^31-byte mark and the end against the FP64 oracle
+    m, k, n, e, top_k = 270000, 4096, 128, 2, 1
+    rng = np.random.default_rng(4096)
+    wp, ws = rand_mxfp4(rng, (e, n), k)
+    g = torch.Generator(device="cuda").manual_seed(4097)
+    a = torch.randn((m, k), generator=g, device="cuda", dtype=torch.bfloat16)
+    ids = torch.randint(0, e, (m, top_k), generator=g, device="cuda")
+    w = torch.rand((m, top_k), generator=g, device="cuda") + 0.5
+    C = torch.full((m, top_k, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    b_scale = torch.tensor([0.5, 1.5], device="cuda")
+    mx.fused_moe_mxfp4_soft(a, cuda(wp), C, torch.tensor([0.75], device="cuda"), b_scale, None,
+                            cuda(ws), w, ids, _empty(), _empty(), _empty(), True, top_k, False,
+                            False)
+    rows = np.array([0, 1, (1 << 31) // (k * 2) - 1, (1 << 31) // (k * 2), m - 2, m - 1])
+    sel = torch.from_numpy(rows).cuda()
+    oracle = O.fused_moe_fp64(a[sel].float().cpu().numpy(), wp, ws, 0.75, b_scale.cpu().numpy(),
+                              w[sel].cpu().numpy(), ids[sel].cpu().numpy(), True)
+    assert not torch.isnan(C).any()
+    assert_parity(C[sel], oracle, what="2.2 GB of activations")
+    del a, C
+    torch.cuda.empty_cache()
+
+
 def test_triton_value_matches_safe_on_the_reference_inputs(monkeypatch):
     # test:144-213 on the test's own inputs (its seed, randn drawn on the
     # device; the reference's quantizer): one expert, top-1, 16 tokens, the
