@@ -125,3 +125,57 @@ def test_graph_soft_op_replays_equal_eager(case, weights):
             torch.cuda.synchronize()
     finally:
         P.unregister_prepacked(w13)
+
+
+def test_concurrent_streams_and_host_threads_equal_sequential(weights):
+    # The library keeps no state between calls but per-device constants and
+    # a thread-local error message; workspaces come with each call.  The MoE
+    # layer and the dense linear on two streams at once, then from two host
+    # threads at once (each on its own stream), give the results of
+    # sequential calls bit for bit.
+    import threading
+    w13, s13, w2, s2, wl, sl = weights
+    cases = []
+    for i, m in enumerate((8, 512)):
+        x = cuda(rand_act(900 + i, (m, 2048)))
+        tw, ti = mx.route_topk(_logits(m, 910 + i), 8)
+        cases.append((x, tw, ti))
+
+    def run(x, tw, ti):
+        return (mx.moe_layer(x, w13, s13, w2, s2, tw, ti), mx.linear_mxfp4_soft(x, wl, sl))
+
+    ref = [run(*c) for c in cases]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rep in range(3):
+        print(f"two streams, round {rep}", flush=True)
+        outs = []
+        for c, s in zip(cases, streams):
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                outs.append(run(*c))
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o[0], r[0]) and torch.equal(o[1], r[1])
+    results, errors = [None, None], []
+
+    def worker(i):
+        try:
+            with torch.cuda.stream(streams[i]):
+                got = [run(*cases[i]) for _ in range(10)]
+            streams[i].synchronize()
+            results[i] = got
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    print("two host threads", flush=True)
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    for got, r in zip(results, ref):
+        assert got is not None and len(got) == 10
+        for o in got:
+            assert torch.equal(o[0], r[0]) and torch.equal(o[1], r[1])
