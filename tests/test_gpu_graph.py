@@ -3,7 +3,8 @@ nothing and records no memset (only kernels), so the router, the MoE layer,
 the dense linear, the soft op and AITER's entry can be captured once and
 replayed with new inputs copied in place.  Every replay must equal eager calls on the same inputs
 bitwise (the kernels are deterministic), with the program's own eager work
-and synchronisations between replays."""
+and synchronisations between replays.  Calls on two streams at once and
+from two host threads at once must equal sequential calls the same way."""
 
 from __future__ import annotations
 
