@@ -200,7 +200,12 @@ int mxfp4_moe_route(const float* logits, int64_t m, int num_experts, int64_t row
  *   e = expert_ids[i] and each route r = sorted_ids[i*block_m + j] <
  *   num_valid:  c[r, :] = a[r / top_k] . dequant(b[e])^T * a_scale[0] *
  *   b_scale[e] (* topk_weights[r] if mul_routed_weight), rounded once to
- *   c_dtype.  Expert -1 writes zeros (aiter:156-172); so does any other id
+ *   c_dtype.  mul_routed_weight is a bit set: bit 0 multiplies the route
+ *   weights; bit 1 (no counterpart in the reference's Triton kernels)
+ *   scales as the reference's safe path rounds, soft:487-494: the sum
+ *   rounded to c_dtype, times a_scale[0] rounded to c_dtype, times
+ *   b_scale[e] rounded to c_dtype, times the route weight in FP32, then
+ *   rounded.  Expert -1 writes zeros (aiter:156-172); so does any other id
  *   outside [0, num_experts).  Rows not named by the metadata are not
  *   written.  a_scale / b_scale may be NULL (= 1).  block_m % 16 == 0;
  *   k % 32 == 0; em = capacity of sorted_ids; expert_ids holds em / block_m

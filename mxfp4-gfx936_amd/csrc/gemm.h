@@ -75,6 +75,9 @@ struct GemmArgs {
   // block-scaled (W4A4) GEMMs: activation format, 0 = packed E2M1, 1 = FP8
   // E4M3, 2 = FP8 E5M2 (FP8 rows are k bytes)
   int32_t a_fp8;
+  // routed plain epilogues: scale as the reference's safe MoE path rounds
+  // (ref_scaled) instead of once
+  int32_t ref_round;
 };
 
 // MFMA operand format code of the block-scaled f8f6f4 instructions for
@@ -162,6 +165,35 @@ __device__ __forceinline__ float scalar_alpha(const GemmArgs& g, int expert) {
   float a = g.a_scale ? g.a_scale[0] : 1.0f;
   if (g.b_scale) a *= g.b_scale[expert];
   return a;
+}
+
+// The reference's safe MoE path in compute dtype OutT (soft:487-494) takes
+// the GEMM's result in OutT, multiplies it by a_scale and rounds to OutT,
+// then by b_scale[e] and rounds to OutT; the route weight (an FP32 tensor)
+// then multiplies in FP32 and the store rounds.  With g.ref_round the
+// plain routed epilogues follow that sequence: the FP32 sum goes through
+// ref_scaled and the epilogue's own scalar becomes 1.  (By default the sum
+// is multiplied by a_scale * b_scale[e] and rounded once, as the
+// reference's Triton kernel does, soft:167-173.)  Identity roundings for
+// OutT = float.
+template <typename OutT>
+__device__ __forceinline__ float ref_scaled(const GemmArgs& g, float acc, int expert) {
+  float v = to_f32(from_f32<OutT>(acc));
+  if (g.a_scale) v = to_f32(from_f32<OutT>(v * g.a_scale[0]));
+  if (g.b_scale) v = to_f32(from_f32<OutT>(v * g.b_scale[expert]));
+  return v;
+}
+
+// ref_scaled over a tile's accumulators (expert >= 0); the epilogue's own
+// scalar is then 1.
+template <typename OutT, int FM, int FN>
+__device__ __forceinline__ void ref_pass(const GemmArgs& g, int expert, f32x4 (&acc)[FM][FN]) {
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i][j][e] = ref_scaled<OutT>(g, acc[i][j][e], expert);
 }
 
 // Host-side launchers (gemm_w4a16.hip, gemm_w4a4.hip).

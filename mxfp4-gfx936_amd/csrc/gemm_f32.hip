@@ -214,7 +214,11 @@ __global__ __launch_bounds__(256) void f32_pipe(GemmArgs g, int nbm, int nbn) {
     if (kt + 1 < nk) step(kt + 1, r0, r1);
   }
 
-  const float alpha = scalar_alpha(g, expert);
+  float alpha = scalar_alpha(g, expert);
+  if (g.ref_round) {
+    ref_pass<float>(g, expert, acc);
+    alpha = 1.0f;
+  }
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll

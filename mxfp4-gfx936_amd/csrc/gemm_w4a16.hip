@@ -49,10 +49,10 @@ __device__ __forceinline__ V zero_v8() {
 // Epilogue for one output element.
 template <typename T, int EPI>
 __device__ __forceinline__ void store_out(const GemmArgs& g, const RowInfo& r, int col,
-                                          float alpha, float v0, float v1) {
+                                          float alpha, float v0, float v1, int expert) {
   T* cp = static_cast<T*>(g.c) + r.out_row * g.ldc + col;
   if (EPI == EPI_STORE) {
-    float o = v0 * alpha;
+    float o = g.ref_round ? ref_scaled<T>(g, v0, expert) : v0 * alpha;
     if (g.route_w) o *= g.route_w[r.out_row];
     if (g.bias) o += to_f32(static_cast<const T*>(g.bias)[col]);
     *cp = from_f32<T>(o);
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(WK * WN * 64) void w4a16_skinny(GemmArgs g) {
       for (int w = 0; w < WK; ++w) s += red[w][cgi][rb * CB + cb][l][i];
       v[cb] = s;
     }
-    store_out<T, EPI>(g, r, col, alpha, v[0], v[CB - 1]);
+    store_out<T, EPI>(g, r, col, alpha, v[0], v[CB - 1], expert);
   }
 }
 
@@ -611,7 +611,7 @@ void w4a16_stream(GemmArgs g) {
         for (int q = 0; q < WK; ++q) acc_s += red[b][q][w][nb][l][i];
         v[nb] = acc_s;
       }
-      store_out<T, EPI>(g, r, col, alpha, v[0], v[NB - 1]);
+      store_out<T, EPI>(g, r, col, alpha, v[0], v[NB - 1], expert);
     }
   });
 }
@@ -773,13 +773,14 @@ __global__ __launch_bounds__(256) void w4a16_tiled(GemmArgs g) {
 #pragma unroll
         for (int fn = 0; fn < FN; fn += 2) {
           const int col = ncol0 + ((wn * FN + fn) >> 1) * 16 + c16;
-          if (col < g.n) store_out<T, EPI>(g, r, col, alpha, acc[fm][fn][i], acc[fm][fn + 1][i]);
+          if (col < g.n) store_out<T, EPI>(g, r, col, alpha, acc[fm][fn][i], acc[fm][fn + 1][i],
+                                         expert);
         }
       } else {
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
           const int col = ncol0 + wn * FN * 16 + fn * 16 + c16;
-          if (col < g.n) store_out<T, EPI>(g, r, col, alpha, acc[fm][fn][i], 0.f);
+          if (col < g.n) store_out<T, EPI>(g, r, col, alpha, acc[fm][fn][i], 0.f, expert);
         }
       }
     }

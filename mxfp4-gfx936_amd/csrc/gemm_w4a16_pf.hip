@@ -442,7 +442,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a16_pf(GemmArgs g, int
   barrier_only();  // every wave is done reading the stage buffers
   // a K slice's partial sums are stored raw; scaling and bias come once,
   // after the slices are summed
-  const float alpha = (EPI == EPI_PARTIAL) ? 1.0f : scalar_alpha(g, expert);
+  float alpha = (EPI == EPI_PARTIAL) ? 1.0f : scalar_alpha(g, expert);
+  if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_F32) {
+    if (g.ref_round) {
+      ref_pass<std::conditional_t<EPI == EPI_STORE_F32, float, T>>(g, expert, acc);
+      alpha = 1.0f;
+    }
+  }
   // the lane's bias values, once (columns past N read as zero)
   constexpr bool kBias = EPI == EPI_STORE || EPI == EPI_STORE_F32;
   float bv[kBias ? FN : 1][4];
@@ -938,7 +944,13 @@ __global__ __launch_bounds__(256, MINB) void w4a16_pp(GemmArgs g, int nbm, int n
     // ---- epilogue: lane holds rows fm*16 + c16, columns fn*16 + grp*4 ..
     // +3 of the wave's 16-column blocks; expert < 0 (not on this device)
     // writes zeros (aiter:156-172)
-    const float alpha = expert >= 0 ? scalar_alpha(g, expert) : 0.f;
+    float alpha = expert >= 0 ? scalar_alpha(g, expert) : 0.f;
+    if constexpr (EPI == EPI_STORE) {
+      if (g.ref_round && expert >= 0) {
+        ref_pass<T>(g, expert, acc);
+        alpha = 1.0f;
+      }
+    }
     // table reads first: the compiler does not move LDS reads across the
     // buffer stores
     uint32_t base[FM];

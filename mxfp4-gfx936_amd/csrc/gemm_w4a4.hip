@@ -176,7 +176,11 @@ __global__ __launch_bounds__(256) void w4a4_tiled(GemmArgs g) {
     __syncthreads();
   }
 
-  const float alpha = scalar_alpha(g, expert);
+  float alpha = scalar_alpha(g, expert);
+  if (g.ref_round) {
+    ref_pass<TO>(g, expert, acc);
+    alpha = 1.0f;
+  }
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
 #pragma unroll

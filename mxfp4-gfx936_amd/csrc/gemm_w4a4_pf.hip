@@ -296,7 +296,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void w4a4_pf(GemmArgs g, int 
   // block (even grp: block 2p, odd grp: block 2p + 1) and writes 16 bytes;
   // a store instruction then covers 64 contiguous bytes of 16 rows.  No LDS
   // staging and no barrier: the tile ends with its stores in flight.
-  const float alpha = scalar_alpha(g, expert);
+  float alpha = scalar_alpha(g, expert);
+  if (g.ref_round) {
+    ref_pass<TO>(g, expert, acc);
+    alpha = 1.0f;
+  }
   const bool vec = (g.ldc % (16 / (int)sizeof(TO))) == 0;
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {

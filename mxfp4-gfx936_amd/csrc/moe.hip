@@ -811,7 +811,10 @@ GemmArgs routed_args(const void* a, int64_t a_rows, int64_t a_row_stride, const 
   g.num_post_padded = num_post_padded;
   g.a_scale = a_scale;
   g.b_scale = b_scale;
-  g.route_w = mul_routed_weight ? topk_weights : nullptr;
+  // mul_routed_weight bit 0: multiply the route weights; bit 1: the
+  // reference safe path's rounding sequence (ref_scaled)
+  g.route_w = (mul_routed_weight & 1) ? topk_weights : nullptr;
+  g.ref_round = (mul_routed_weight >> 1) & 1;
   g.m = em;
   g.num_valid = num_valid;
   g.n = (int32_t)n;

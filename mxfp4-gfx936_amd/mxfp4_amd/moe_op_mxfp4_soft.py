@@ -58,6 +58,20 @@ def _backend() -> str:
     return backend
 
 
+def _reference_rounding() -> bool:
+    """``MXFP4_GFX950_ROUNDING``: ``once`` (default) scales the FP32 sum by
+    a_scale * b_scale[e] (* route weight) and rounds once to C's dtype, as
+    the reference's Triton kernel does (soft:167-173); ``reference`` makes
+    the safe value follow the reference safe path's sequence instead
+    (soft:487-494: the GEMM result rounded to C's dtype, times a_scale and
+    rounded, times b_scale[e] and rounded, times the route weight in FP32
+    and rounded).  Anything else fails loudly."""
+    mode = os.getenv("MXFP4_GFX950_ROUNDING", "once")
+    if mode not in ("once", "reference"):
+        raise ValueError(f"unknown MXFP4_GFX950_ROUNDING: {mode}")
+    return mode == "reference"
+
+
 def _require_triton_compiler() -> None:
     """soft:52-57: the ``triton`` backend value fails loudly, with the
     reference's message, when ``_has_compatible_triton_compiler`` says no
@@ -403,6 +417,8 @@ def fused_moe_mxfp4_soft(
                                    mul_routed_weight, top_k, block_m)
         return
     del sorted_token_ids, expert_ids, num_tokens_post_padded
+    # bit 0: route weights; bit 1: the safe path's rounding sequence
+    flags = (1 if mul_routed_weight else 0) | (2 if _reference_rounding() else 0)
     # operand checks first (soft:468-477), then the device
     act, act_mx, b, b_mx, a_scale, b_scale, weights, ids = _prepare_moe_operands(
         A, B, C, A_scale, B_scale, A_mx_scale, B_mx_scale, topk_weights, topk_ids, top_k)
@@ -426,7 +442,7 @@ def fused_moe_mxfp4_soft(
             _lib.ptr(act), a_code, act.shape[0], act.stride(0), _lib.ptr(act_mx), _lib.ptr(b),
             _lib.ptr(b_mx), _lib.ptr(pre_b), _lib.ptr(pre_s), num_experts, n, k, _lib.ptr(out),
             c_code, _lib.ptr(a_scale),
-            _lib.ptr(b_scale), _lib.ptr(weights), 1 if mul_routed_weight else 0, _lib.ptr(ids),
+            _lib.ptr(b_scale), _lib.ptr(weights), flags, _lib.ptr(ids),
             _lib.dtype_code(ids.dtype), m, top_k, _lib.ptr(ws), ws_bytes,
             _lib.stream_of(device)))
     if out is not C:

@@ -117,6 +117,17 @@ def test_backend_env(monkeypatch):
     assert soft._backend() == "triton"
 
 
+def test_rounding_env(monkeypatch):
+    from mxfp4_amd import moe_op_mxfp4_soft as soft
+    monkeypatch.delenv("MXFP4_GFX950_ROUNDING", raising=False)
+    assert soft._reference_rounding() is False
+    monkeypatch.setenv("MXFP4_GFX950_ROUNDING", "reference")
+    assert soft._reference_rounding() is True
+    monkeypatch.setenv("MXFP4_GFX950_ROUNDING", "twice")
+    with pytest.raises(ValueError, match="MXFP4_GFX950_ROUNDING"):
+        soft._reference_rounding()
+
+
 def test_soft_module_loads_by_path_like_the_reference_tests():
     spec = importlib.util.spec_from_file_location("moe_op_mxfp4_soft", SOFT)
     module = importlib.util.module_from_spec(spec)

@@ -91,6 +91,50 @@ def _bf16_ulp_distance(a, b):
 @pytest.mark.parametrize("m_value", [1, 2, 4, 8, 64])
 @pytest.mark.parametrize("quantize_activations", [False, True])
 @pytest.mark.parametrize("mul_routed_weight", [False, True])
+def test_fused_moe_matrix_reference_rounding(m_value, quantize_activations, mul_routed_weight,
+                                             monkeypatch):
+    # MXFP4_GFX950_ROUNDING=reference: the safe path's rounding sequence
+    # (soft:487-494), which the per-(token, slot) loop shares but for its
+    # GEMV's summation order -- so the reference's own bar (test:283-285,
+    # rtol=atol=1e-2) holds on the test's own inputs, and results sit within
+    # one bf16 step of the loop's (a sum on the other side of a rounding
+    # boundary) carried through the scalar multiplies
+    monkeypatch.setenv("MXFP4_GFX950_ROUNDING", "reference")
+    torch.manual_seed(20260810 + m_value)
+    n_value, k_value, experts, top_k = 64, 128, 4, 2
+    activations = torch.randn((m_value, k_value), device="cuda", dtype=torch.bfloat16)
+    weights = torch.randn((experts, n_value, k_value), device="cuda", dtype=torch.bfloat16)
+    wp, ws = (cuda(t) for t in O.quant_mxfp4_ties_away(weights.float().cpu().numpy()))
+    dq = mx.dequant_mxfp4(wp, ws, torch.bfloat16)
+    if quantize_activations:
+        ap, asc = O.quant_mxfp4_ties_away(activations.float().cpu().numpy())
+        kernel_a, kernel_amx = cuda(ap), cuda(asc)
+        ref_a = mx.dequant_mxfp4(kernel_a, kernel_amx, torch.bfloat16)
+    else:
+        kernel_a, kernel_amx, ref_a = activations, None, activations
+    logits = torch.randn((m_value, experts), device="cuda", dtype=torch.float32)
+    topk_weights, topk_ids = torch.topk(torch.softmax(logits, dim=-1), k=top_k, dim=-1)
+    actual = torch.empty((m_value, top_k, n_value), device="cuda", dtype=torch.bfloat16)
+    scalar_a = torch.tensor([0.75], device="cuda", dtype=torch.float32)
+    scalar_b = torch.linspace(0.5, 1.25, experts, device="cuda")
+    mx.fused_moe_mxfp4_soft(kernel_a, wp, actual, scalar_a, scalar_b, kernel_amx, ws,
+                            topk_weights, topk_ids, _empty(), _empty(), _empty(),
+                            mul_routed_weight, top_k, False, False)
+    expected = torch.empty_like(actual)
+    for t in range(m_value):
+        for s in range(top_k):
+            e = int(topk_ids[t, s])
+            v = torch.matmul(ref_a[t], dq[e].transpose(0, 1)) * scalar_a[0] * scalar_b[e]
+            if mul_routed_weight:
+                v = v * topk_weights[t, s]
+            expected[t, s] = v.to(expected.dtype)
+    torch.testing.assert_close(actual, expected, rtol=1e-2, atol=1e-2)
+    assert int(_bf16_ulp_distance(actual, expected).max()) <= 2
+
+
+@pytest.mark.parametrize("m_value", [1, 2, 4, 8, 64])
+@pytest.mark.parametrize("quantize_activations", [False, True])
+@pytest.mark.parametrize("mul_routed_weight", [False, True])
 def test_fused_moe_matrix_reference_inputs(m_value, quantize_activations, mul_routed_weight):
     # The operator matrix on the very inputs the reference's test draws
     # (test:219-243: torch.manual_seed(20260810 + m), then randn on the
