@@ -367,7 +367,9 @@ def fused_moe_mxfp4_soft(
     slot s) whose expert e = topk_ids[t, s] is in [0, E):
     C[t, s] = A[t] . dequant(B[e])^T * A_scale[0] * B_scale[e]
     (* topk_weights[t, s] when ``mul_routed_weight``), FP32 accumulation, one
-    rounding to C.dtype.  A is bf16/fp16/fp32 (converted to C.dtype, soft:475)
+    rounding to C.dtype (with ``MXFP4_GFX950_ROUNDING=reference`` the safe
+    path's own rounding sequence, soft:487-494; see ``_reference_rounding``).
+    A is bf16/fp16/fp32 (converted to C.dtype, soft:475)
     or packed MXFP4 with ``A_mx_scale`` (W4A4 on the block-scaled MFMA).
     Like the reference's safe path, the routing metadata arguments are not
     consulted (soft:466): one library call builds the routing on the device
